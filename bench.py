@@ -1,0 +1,366 @@
+"""Benchmark: attention2d & matmul2d TFLOP/s (+% of MFMA peak) on 1 MI355X vs host CPU.
+
+Headline workload: matmul2d fp32, one step = one
+1024^3 GEMM plus one 1000x1030x777 GEMM, inputs resident in HBM (uploaded
+once through resident sessions), launch-only.  `value` = algorithmic FLOPs of
+the timed steps / wall time of the timed region (hipEvents on the backend
+stream, device synchronised on both sides).
+
+Also reported (`per_config`): every other BASELINE config on its own resident
+launch-only loop, each with TFLOP/s (or GB/s for the HBM-bound skinny GEMM)
+and its fraction of the gfx950 peak, plus a bounded CPU-baseline sample.
+
+The CPU baseline runs the reference's own CPU path (oracle/_ref/libref.so,
+compiled from the reference sources) when present, else this build's C
+restatement (oracle/liboracle.so), single-threaded, on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras]
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "lightining-core_amd"))
+
+METRIC = "attention2d & matmul2d TFLOP/s (+% of MFMA peak) on 1 MI355X vs host CPU"
+PEAK_TFLOPS = {"f32": 157.3, "bf16": 2516.6, "f16": 2516.6}  # gfx950 dense MFMA (2.4 GHz)
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# GPU timing on the backend stream
+# ---------------------------------------------------------------------------
+
+def timed(lc, fn, iters):
+    """hipEvents on the backend stream around `fn(iters)`; device synced on both sides."""
+    lc.device_synchronize()
+    t = lc.HipTimer()
+    t.start()
+    fn(iters)
+    ms = t.stop()
+    lc.device_synchronize()
+    t.close()
+    return ms
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (reference CPU path or this build's restatement)
+# ---------------------------------------------------------------------------
+
+class CpuBaseline:
+    def __init__(self):
+        ref = os.path.join(ROOT, "oracle", "_ref", "libref.so")
+        orc = os.path.join(ROOT, "oracle", "liboracle.so")
+        P, S = ctypes.c_void_p, ctypes.c_size_t
+        self.lib = None
+        if os.path.exists(ref):
+            self.lib = ctypes.CDLL(ref)
+            self.kind = "reference"
+            self.lib.ref_matmul.argtypes = [P, P, P, S, S, S]
+            self.lib.ref_attention_forward.argtypes = [P, P, P, P, S, S, ctypes.c_int, ctypes.c_float,
+                                                       ctypes.c_float, ctypes.c_int]
+        if os.path.exists(orc):
+            self.orc = ctypes.CDLL(orc)
+            self.orc.orc_matmul_rows.argtypes = [P, P, P, S, S, S, S, S]
+            self.orc.orc_attention_forward_rows.argtypes = [P, P, P, P, S, S, ctypes.c_int, S, S]
+            self.orc.orc_vit_block.argtypes = [P] * 5 + [S] * 9
+            if self.lib is None:
+                self.kind = "port"
+        else:
+            self.orc = None
+        if self.lib is None and self.orc is None:
+            self.kind = None
+
+    @staticmethod
+    def _p(a):
+        return a.ctypes.data_as(ctypes.c_void_p)
+
+    def matmul(self, a, b):
+        m, k = a.shape
+        n = b.shape[1]
+        out = np.empty((m, n), np.float32)
+        if self.kind == "reference":
+            self.lib.ref_matmul(self._p(a), self._p(b), self._p(out), m, k, n)
+        else:
+            self.orc.orc_matmul_rows(self._p(a), self._p(b), self._p(out), m, k, n, 0, m)
+        return out
+
+    def matmul_rows(self, a, b, r0, r1):
+        """Port rows subset (the reference entry has no row range)."""
+        m, k = a.shape
+        n = b.shape[1]
+        out = np.empty((r1 - r0, n), np.float32)
+        self.orc.orc_matmul_rows(self._p(a), self._p(b), self._p(out), m, k, n, r0, r1)
+        return out
+
+    def attention(self, q, k, v, causal):
+        s, d = q.shape
+        out = np.empty_like(q)
+        if self.kind == "reference":
+            self.lib.ref_attention_forward(self._p(q), self._p(k), self._p(v), self._p(out), s, d, int(causal), 1.0,
+                                           0.0, 0)
+        else:
+            self.orc.orc_attention_forward_rows(self._p(q), self._p(k), self._p(v), self._p(out), s, d, int(causal),
+                                                0, s)
+        return out
+
+    def attention_rows(self, q, k, v, causal, r0, r1):
+        s, d = q.shape
+        out = np.empty((r1 - r0, d), np.float32)
+        self.orc.orc_attention_forward_rows(self._p(q), self._p(k), self._p(v), self._p(out), s, d, int(causal), r0,
+                                            r1)
+        return out
+
+
+def cpu_threads_used():
+    return 1
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+def bench_config2(lc, synth, steps, warmup, cpu):
+    """Headline: fp32 GEMM 1024^3 + 1000x1030x777."""
+    shapes = [(1024, 1024, 1024), (1000, 777, 1030)]
+    sess, inputs = [], []
+    for i, (m, k, n) in enumerate(shapes):
+        a = synth.uniform((m, k), stream=100 + 2 * i)
+        b = synth.uniform((k, n), stream=101 + 2 * i)
+        s = lc.MatMulResidentSession(m, k, n, "f32")
+        s.start_into(a, b)
+        sess.append(s)
+        inputs.append((a, b))
+    lc.device_synchronize()
+    flops_step = sum(2.0 * m * k * n for m, k, n in shapes)
+
+    def step_loop(iters):
+        for _ in range(iters):
+            for s in sess:
+                s.run_into()
+
+    step_loop(warmup)
+    ms = timed(lc, step_loop, steps)
+    ms_per_step = ms / steps
+    value = flops_step / (ms_per_step * 1e-3) / 1e12
+
+    # dominant kernel (1024^3 GEMM) alone, back-to-back launches
+    reps = max(50, steps)
+    sess[0].run_batch_sync_cached_no_download(5)
+    kms = timed(lc, lambda it: sess[0].run_batch_sync_cached_no_download(it), reps) / reps
+    kflops = 2.0 * 1024 ** 3
+    achieved = kflops / (kms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": "gemm_f32_kernel (1024^3, v_mfma_f32_32x32x2_f32)",
+                "achieved": round(achieved, 3), "peak": PEAK_TFLOPS["f32"], "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_TFLOPS["f32"], 4), "traffic": None,
+                "avg_kernel_ms": round(kms, 5), "algorithmic_flops_per_launch": int(kflops)}
+
+    cpu_obj = None
+    if cpu.kind is not None:
+        log(f"[bench] cpu baseline ({cpu.kind}) on config 2 ...")
+        t0 = time.perf_counter()
+        reps_done, flops_done = 0, 0.0
+        while True:
+            for (m, k, n), (a, b) in zip(shapes, inputs):
+                cpu.matmul(a, b)
+                flops_done += 2.0 * m * k * n
+            reps_done += 1
+            el = time.perf_counter() - t0
+            if el >= 10.0 or reps_done >= 30:
+                break
+        cpu_obj = {"value": round(flops_done / el / 1e12, 6), "unit": "TFLOP/s", "cores": cpu_threads_used(),
+                   "kind": cpu.kind,
+                   "sample": f"{reps_done} full steps (1024^3 + 1000x1030x777 fp32 GEMM) in {el:.1f} s, "
+                             "single thread, -O3 -ffast-math -funroll-loops"}
+    # free device memory before the large extras
+    for s in sess:
+        s.close()
+    return value, ms_per_step, roofline, cpu_obj
+
+
+def extra_entry(name, flops, ms, dtype, cpu_tflops=None, cpu_sample=None, bytes_=None, bound="mfma"):
+    e = {"ms": round(ms, 5)}
+    if bound == "hbm":
+        gbs = bytes_ / (ms * 1e-3) / 1e9
+        e.update({"GB/s": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
+                  "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 3)})
+    else:
+        tf = flops / (ms * 1e-3) / 1e12
+        e.update({"TFLOP/s": round(tf, 3), "frac_peak": round(tf / PEAK_TFLOPS[dtype], 4),
+                  "peak": PEAK_TFLOPS[dtype]})
+    e["dtype"] = dtype
+    if cpu_tflops is not None:
+        e["cpu_TFLOP/s"] = cpu_tflops
+        e["cpu_sample"] = cpu_sample
+    log(f"[bench] {name}: {e}")
+    return e
+
+
+def bench_extras(lc, synth, cpu):
+    out = {}
+    # C1 attention fp32 S=256 D=64
+    s, d = 256, 64
+    q, k, v = (synth.normal((s, d), stream=200 + i) for i in range(3))
+    sess = lc.AttentionSession(s, d, causal=False)
+    sess.forward_with_policy(q, k, v, lc.AttentionIoPolicy(download_out=False))
+    sess.run_cached(20)
+    iters = 200
+    ms = timed(lc, sess.run_cached, iters) / iters
+    cpu_tf = sample = None
+    if cpu.kind is not None:
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 1.0:
+            cpu.attention(q, k, v, False)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu_tf = round(n * 4.0 * s * s * d / el / 1e12, 6)
+        sample = f"{n} full forwards in {el:.2f} s, 1 thread ({cpu.kind})"
+    out["C1_attention_f32_S256_D64"] = extra_entry("C1", 4.0 * s * s * d, ms, "f32", cpu_tf, sample)
+    sess.close()
+
+    # C3 attention bf16 causal B4 H16 S2048 D128
+    b, h, s, d = 4, 16, 2048, 128
+    shape = (b, h, s, d)
+    q, k, v = (0.5 * synth.normal(shape, stream=210 + i) for i in range(3))
+    sess = lc.AttentionSession.batched(b, h, s, d, causal=True, compute_dtype="bf16")
+    sess.forward_with_policy(q, k, v, lc.AttentionIoPolicy(download_out=False))
+    sess.run_cached(3)
+    iters = 20
+    ms = timed(lc, sess.run_cached, iters) / iters
+    flops = 4.0 * d * s * (s + 1) / 2 * b * h
+    cpu_tf = sample = None
+    if cpu.orc is not None:
+        qr, kr, vr = (synth.round_bf16(x[0, 0]) for x in (q, k, v))
+        rows = 32
+        t0 = time.perf_counter()
+        for r in np.linspace(0, s - 1, rows).astype(int):
+            cpu.attention_rows(qr, kr, vr, True, int(r), int(r) + 1)
+        el = time.perf_counter() - t0
+        est = el * (s / rows) * b * h
+        cpu_tf = round(flops / est / 1e12, 6)
+        sample = f"{rows} evenly spaced query rows of one head in {el:.2f} s, scaled x{s // rows * b * h} (port)"
+    out["C3_attention_bf16_causal_B4_H16_S2048_D128"] = extra_entry("C3", flops, ms, "bf16", cpu_tf, sample)
+    sess.close()
+    del q, k, v
+
+    # C4 ViT block fp16
+    bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12
+    x = synth.uniform((bn, c, img, img), lo=0.0, hi=1.0, stream=220)
+    w_conv = synth.normal((e, c, p, p), std=0.02, stream=221)
+    w_qkv = synth.normal((e, 3 * e), std=0.02, stream=222)
+    w_o = synth.normal((e, e), std=0.02, stream=223)
+    vs = lc.VitBlockSession(bn, c, img, img, p, e, heads, "f16")
+    vs.set_weights(w_conv, w_qkv, w_o)
+    vs.forward(x, download=False)
+    vs.run_cached(5)
+    iters = 50
+    ms = timed(lc, vs.run_cached, iters) / iters
+    t_ = (img // p) ** 2
+    flops = (2.0 * bn * t_ * e * c * p * p + 2.0 * bn * t_ * e * 3 * e + 4.0 * bn * heads * t_ * t_ * (e // heads)
+             + 2.0 * bn * t_ * e * e)
+    cpu_tf = sample = None
+    if cpu.orc is not None:
+        rs = [synth.round_f16(a) for a in (x, w_conv, w_qkv, w_o)]
+        out_rows = np.empty((t_, e), np.float32)
+        P = ctypes.c_void_p
+        t0 = time.perf_counter()
+        cpu.orc.orc_vit_block(*(a.ctypes.data_as(P) for a in rs), out_rows.ctypes.data_as(P), bn, c, img, img, p, e,
+                              heads, 0, t_)
+        el = time.perf_counter() - t0
+        cpu_tf = round(flops / (el * bn) / 1e12, 6)
+        sample = f"one image of 8 (196 token rows) in {el:.2f} s, scaled x8 (port)"
+    out["C4_vit_block_f16_B8"] = extra_entry("C4", flops, ms, "f16", cpu_tf, sample)
+    vs.close()
+
+    # C5 bf16 GEMM sweep, 100 launches in a resident session
+    for m, k, n in ((4096, 4096, 4096), (8192, 8192, 8192), (16, 8192, 8192)):
+        a = synth.normal((m, k), stream=230)
+        bm = synth.normal((k, n), stream=231)
+        sess = lc.MatMulResidentSession(m, k, n, "bf16")
+        sess.start_into(a, bm)
+        sess.run_batch_sync_cached_no_download(10)
+        iters = 100
+        ms = timed(lc, sess.run_batch_sync_cached_no_download, iters) / iters
+        flops = 2.0 * m * k * n
+        cpu_tf = sample = None
+        if cpu.orc is not None:
+            rows = min(m, 16 if m > 16 else m)
+            ar, br = synth.round_bf16(a), synth.round_bf16(bm)
+            t0 = time.perf_counter()
+            cpu.matmul_rows(ar, br, 0, rows)
+            el = time.perf_counter() - t0
+            cpu_tf = round(flops / (el * m / rows) / 1e12, 6)
+            sample = f"{rows} rows in {el:.2f} s, scaled x{m // rows} (port)"
+        if m == 16:
+            bytes_ = m * k * 2 + k * n * 2 + m * n * 4
+            out["C5c_gemm_bf16_16x8192x8192"] = extra_entry("C5c", flops, ms, "bf16", cpu_tf, sample, bytes_, "hbm")
+        else:
+            out[f"C5_gemm_bf16_{m}^3"] = extra_entry(f"C5 {m}", flops, ms, "bf16", cpu_tf, sample)
+        sess.close()
+        del a, bm
+    return out
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-extras", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        log("bench.py: this build measures one GPU only (the path is single-GPU; see DESIGN.md for how it would "
+            "shard); run with --gpus 1")
+        sys.exit(2)
+
+    import lightning_core as lc
+    from lightning_core import synth
+
+    if not lc.is_hip_available():
+        log("bench.py: no gfx950 HIP device visible")
+        sys.exit(1)
+    info = lc.device_info()
+    log(f"[bench] device {info}")
+    cpu = CpuBaseline()
+    value, ms_per_step, roofline, cpu_obj = bench_config2(lc, synth, args.steps, args.warmup, cpu)
+    log(f"[bench] config2: {value:.3f} TFLOP/s, {ms_per_step:.4f} ms/step, kernel {roofline}")
+    extras = {} if args.no_extras else bench_extras(lc, synth, cpu)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 4),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: SplitMix64 U(-1,1), seed 20260401, inputs resident in HBM",
+        "config": {"workload": "configs[1]: matmul2d fp32 GEMM 1024x1024x1024 + 1000x1030x777 per step, "
+                               "resident sessions, launch-only",
+                   "parallelism": "single GPU", "device": info["name"], "arch": info["gcn_arch"],
+                   "compute_units": info["compute_units"]},
+        "roofline": roofline,
+        "cpu_baseline": cpu_obj,
+        "per_config": extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

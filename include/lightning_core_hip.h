@@ -1,0 +1,419 @@
+/*
+ * lightning_core_hip.h -- C ABI of the MI355X (gfx950) backend for Lightning Core.
+ *
+ * Part 1 restates the reference's frozen C ABI
+ * (include/lightning_core/lightning_core.h:1-141 in the reference tree):
+ * identical function signatures and struct layouts, with LC_DEVICE_HIP
+ * appended to lcDeviceKind after LC_DEVICE_METAL without renumbering.
+ *
+ * Part 2 adds the compute entry points.  The reference's C ABI has none; each
+ * one below is the C form of a C++/pybind entry point of the reference and
+ * cites it.  Plain pointers and sizes only.  Host pointers are caller-owned;
+ * device buffers are owned by the library (sessions own theirs).
+ *
+ * Only the "hip" device computes in this library.  Requests for cpu / cuda /
+ * metal compute return LC_NOT_SUPPORTED: those devices are served by the
+ * reference's own backends, and this library never computes on the CPU.
+ * Errors: LC_INVALID_VALUE for null pointers a policy requires or zero sizes;
+ * LC_NOT_SUPPORTED when no gfx950 device is visible or a shape / dtype is
+ * outside what the kernels handle; LC_DRIVER_ERROR / LC_OUT_OF_MEMORY from HIP.
+ * lcGetLastErrorMessage() returns a human-readable reason for the last error.
+ */
+#ifndef LIGHTNING_CORE_HIP_H
+#define LIGHTNING_CORE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define LC_API_VERSION_MAJOR 0
+#define LC_API_VERSION_MINOR 6
+#define LC_API_VERSION_PATCH 0
+#define LC_API_VERSION_STRING "0.6.0-rc0"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ===== Part 1: the reference's C ABI (lightning_core.h:14-137) ============== */
+
+typedef enum lcError {
+  LC_SUCCESS = 0,
+  LC_NOT_INITIALIZED,
+  LC_INVALID_VALUE,
+  LC_OUT_OF_MEMORY,
+  LC_NOT_SUPPORTED,
+  LC_DRIVER_ERROR,
+  LC_UNKNOWN
+} lcError_t;
+
+typedef enum lcMemcpyKind {
+  LC_MEMCPY_HOST_TO_HOST = 0,
+  LC_MEMCPY_HOST_TO_DEVICE,
+  LC_MEMCPY_DEVICE_TO_HOST,
+  LC_MEMCPY_DEVICE_TO_DEVICE
+} lcMemcpyKind;
+
+/* lightning_core.h:31-35, with LC_DEVICE_HIP appended (= 3). */
+typedef enum lcDeviceKind {
+  LC_DEVICE_CPU = 0,
+  LC_DEVICE_CUDA,
+  LC_DEVICE_METAL,
+  LC_DEVICE_HIP
+} lcDeviceKind;
+
+typedef enum lcMemoryModel {
+  LC_MEMORY_NATIVE_DEVICE = 0,
+  LC_MEMORY_HOST_MANAGED_COMPAT
+} lcMemoryModel;
+
+typedef enum lcSyncMode {
+  LC_SYNC_AUTO = 0,
+  LC_SYNC_ALWAYS,
+  LC_SYNC_NEVER
+} lcSyncMode;
+
+typedef struct lcSyncPolicy {
+  lcSyncMode mode;
+  int trace_sync_boundary;
+} lcSyncPolicy;
+
+typedef struct lcBackendCapabilities {
+  lcDeviceKind device;
+  int built;
+  int available;
+  int compute_surface;
+  int memory_surface;
+  int sync_surface;
+  int profiling_surface;
+  int runtime_trace_surface;
+  int sync_policy_surface;
+  lcMemoryModel memory_model;
+} lcBackendCapabilities;
+
+typedef struct lcComputeInterfaceContract {
+  int available;
+  int op_dispatch_trace_surface;
+  const char* driver_tag;
+} lcComputeInterfaceContract;
+
+typedef struct lcMemoryInterfaceContract {
+  int available;
+  int allocator_surface;
+  int memcpy_surface;
+  lcMemoryModel memory_model;
+  const char* driver_tag;
+} lcMemoryInterfaceContract;
+
+typedef struct lcSyncInterfaceContract {
+  int available;
+  int sync_policy_surface;
+  int trace_sync_boundary_surface;
+  const char* driver_tag;
+} lcSyncInterfaceContract;
+
+typedef struct lcProfilerInterfaceContract {
+  int available;
+  int runtime_trace_surface;
+  int op_dispatch_trace_surface;
+  size_t trace_capacity;
+  const char* driver_tag;
+} lcProfilerInterfaceContract;
+
+typedef struct lcBackendInterfaceContract {
+  lcDeviceKind device;
+  lcBackendCapabilities capabilities;
+  lcComputeInterfaceContract compute;
+  lcMemoryInterfaceContract memory;
+  lcSyncInterfaceContract sync;
+  lcProfilerInterfaceContract profiler;
+} lcBackendInterfaceContract;
+
+typedef enum lcStructId {
+  LC_STRUCT_BACKEND_CAPABILITIES = 1,
+  LC_STRUCT_COMPUTE_INTERFACE_CONTRACT = 2,
+  LC_STRUCT_MEMORY_INTERFACE_CONTRACT = 3,
+  LC_STRUCT_SYNC_INTERFACE_CONTRACT = 4,
+  LC_STRUCT_PROFILER_INTERFACE_CONTRACT = 5,
+  LC_STRUCT_BACKEND_INTERFACE_CONTRACT = 6
+} lcStructId;
+
+/* lightning_core.h:113-137; lcMalloc/lcFree -> hipMalloc/hipFree,
+ * lcMemcpy -> hipMemcpy kinds, lcDeviceSynchronize -> backend stream sync. */
+lcError_t lcMalloc(void** ptr, size_t size_bytes);
+lcError_t lcFree(void* ptr);
+lcError_t lcMemcpy(void* dst, const void* src, size_t size_bytes, lcMemcpyKind kind);
+lcError_t lcDeviceSynchronize(void);
+lcError_t lcGetDeviceCount(int* count);
+lcError_t lcGetPreferredDeviceForInference(lcDeviceKind* device);
+lcError_t lcGetPreferredDeviceForTraining(lcDeviceKind* device);
+int lcIsCudaAvailable(void);
+int lcIsMetalAvailable(void);
+lcMemoryModel lcGetMemoryModel(void);
+const char* lcGetMemoryModelName(lcMemoryModel model);
+lcError_t lcSetDefaultSyncPolicy(lcSyncPolicy policy);
+lcSyncPolicy lcGetDefaultSyncPolicy(void);
+lcError_t lcApplySyncPolicy(lcSyncPolicy policy);
+lcError_t lcApplyDefaultSyncPolicy(void);
+lcError_t lcGetBackendCapabilities(lcDeviceKind device, lcBackendCapabilities* out_caps);
+lcError_t lcGetActiveBackendCapabilities(lcBackendCapabilities* out_caps);
+lcError_t lcGetBackendInterfaceContract(lcDeviceKind device, lcBackendInterfaceContract* out_contract);
+lcError_t lcGetActiveBackendInterfaceContract(lcBackendInterfaceContract* out_contract);
+lcError_t lcGetApiVersion(int* out_major, int* out_minor, int* out_patch);
+const char* lcGetApiVersionString(void);
+size_t lcGetStructSize(lcStructId struct_id);
+int lcCheckStructSize(lcStructId struct_id, size_t observed_size);
+const char* lcBackendName(void);
+const char* lcGetErrorString(lcError_t error);
+
+/* ===== Part 2: HIP backend additions ======================================== */
+
+/* Parallels lcIsCudaAvailable / lcIsMetalAvailable (lightning_core.h:120-121):
+ * 1 when a gfx950 device is visible to HIP. */
+int lcIsHipAvailable(void);
+
+/* Human-readable reason for the last non-success status returned on this
+ * thread (empty string when none). */
+const char* lcGetLastErrorMessage(void);
+
+/* --- runtime trace (reference runtime.hpp:49-83, :222-257) ----------------- */
+
+typedef struct lcRuntimeTraceEvent {
+  int type;              /* RuntimeTraceEventType (runtime.hpp:50-62) */
+  lcError_t status;
+  uint64_t timestamp_ns; /* steady clock */
+  size_t size_bytes;     /* bytes, or the op's workload hint for op_dispatch */
+  int detail0;           /* op kind for op_dispatch (runtime.hpp:65-73) */
+  int detail1;           /* requested | selected << 4 | fallback << 8 */
+} lcRuntimeTraceEvent;
+
+void lcSetRuntimeTraceEnabled(int enabled);                                  /* runtime.hpp:223 */
+int lcIsRuntimeTraceEnabled(void);                                           /* runtime.hpp:226 */
+void lcClearRuntimeTraceEvents(void);                                        /* runtime.hpp:229 */
+size_t lcGetRuntimeTraceEvents(lcRuntimeTraceEvent* out, size_t capacity);   /* runtime.hpp:232; returns count */
+size_t lcGetRuntimeTraceEventCapacity(void);                                 /* runtime.hpp:235 */
+const char* lcRuntimeTraceEventTypeName(int type);                           /* runtime.hpp:238 */
+const char* lcRuntimeTraceOpKindName(int op);                                /* runtime.hpp:241 */
+int lcEncodeRuntimeTraceDispatchDetail(lcDeviceKind requested, lcDeviceKind selected, int fallback); /* :244 */
+int lcDecodeRuntimeTraceDispatchDetail(int encoded, lcDeviceKind* requested, lcDeviceKind* selected,
+                                       int* fallback);                       /* runtime.hpp:247-250 */
+
+/* --- compute dtype (new surface: the reference API is fp32-only) ---------- */
+
+typedef enum lcDataType {
+  LC_DTYPE_F32 = 0,  /* fp32 storage, fp32 MFMA */
+  LC_DTYPE_BF16 = 1, /* bf16 storage, bf16 MFMA, fp32 accumulate */
+  LC_DTYPE_F16 = 2   /* fp16 storage, fp16 MFMA, fp32 accumulate */
+} lcDataType;
+
+/* --- attention forward ------------------------------------------------------ */
+
+/* AttentionConfig (reference include/lightning_core/core/attention.hpp:9-13). */
+typedef struct lcAttentionConfig {
+  size_t seq_len;
+  size_t head_dim;
+  int causal;
+} lcAttentionConfig;
+
+/* AttentionIoPolicy (attention.hpp:16-32); defaults from lcAttentionIoPolicyDefault(). */
+typedef struct lcAttentionIoPolicy {
+  int upload_q;
+  int upload_k;
+  int upload_v;
+  int upload_target;
+  int download_out;
+  int download_v;
+  int synchronize;
+  int loss_every;
+  float output_scale;
+  float output_bias;
+  int output_relu;
+} lcAttentionIoPolicy;
+
+lcAttentionIoPolicy lcAttentionIoPolicyDefault(void);
+
+/* attentionImplementationName (src/attention.cpp:108-120): "custom-hip-mfma-flash"
+ * for LC_DEVICE_HIP when available. */
+const char* lcAttentionImplementationName(lcDeviceKind device);
+
+/* attentionForward (src/attention.cpp:127-135): q, k, v, out are host [S, D] fp32. */
+lcError_t lcAttentionForward(const float* q, const float* k, const float* v, float* out,
+                             const lcAttentionConfig* cfg, lcDeviceKind device);
+
+/* attentionForwardWithPolicy (src/attention.cpp:137-201).  Validation order,
+ * workload hint (S*S*D), postprocess out = relu?(out*scale + bias) and the
+ * op_dispatch trace follow the reference. */
+lcError_t lcAttentionForwardWithPolicy(const float* q, const float* k, const float* v, float* out,
+                                       const lcAttentionConfig* cfg, lcDeviceKind device,
+                                       const lcAttentionIoPolicy* policy);
+
+/* Batched multi-head attention (new surface; the reference has only the 2-D
+ * single-head entry, so this is attentionForwardWithPolicy over batch*heads
+ * independent problems).  q, k, v, out: host fp32 [batch, heads, S, D];
+ * inputs are rounded to compute_dtype on upload (RNE); fp32 accumulate; out fp32. */
+typedef struct lcAttentionBatchedConfig {
+  size_t batch;
+  size_t heads;
+  size_t seq_len;
+  size_t head_dim;
+  int causal;
+  lcDataType compute_dtype;
+} lcAttentionBatchedConfig;
+
+lcError_t lcAttentionForwardBatched(const float* q, const float* k, const float* v, float* out,
+                                    const lcAttentionBatchedConfig* cfg, lcDeviceKind device,
+                                    const lcAttentionIoPolicy* policy);
+
+/* AttentionSession (attention.hpp:86-129, src/attention.cpp:247-283): binds
+ * the shape and device and owns persistent device buffers, so upload_q/k/v = 0
+ * reuses the resident inputs (upload once, launch only) and download_out = 0
+ * leaves the result on the device.  Sessions default to synchronize = 0, as
+ * the reference's Metal sessions do (src/attention.cpp:249-253). */
+typedef struct lcAttentionSession lcAttentionSession;
+
+lcError_t lcAttentionSessionCreate(const lcAttentionConfig* cfg, lcDeviceKind device, lcAttentionSession** out);
+lcError_t lcAttentionSessionCreateBatched(const lcAttentionBatchedConfig* cfg, lcDeviceKind device,
+                                          lcAttentionSession** out);
+lcError_t lcAttentionSessionDestroy(lcAttentionSession* session);
+lcError_t lcAttentionSessionSetDefaultPolicy(lcAttentionSession* session, const lcAttentionIoPolicy* policy);
+lcError_t lcAttentionSessionGetDefaultPolicy(const lcAttentionSession* session, lcAttentionIoPolicy* out);
+lcError_t lcAttentionSessionForward(lcAttentionSession* session, const float* q, const float* k, const float* v,
+                                    float* out);
+lcError_t lcAttentionSessionForwardWithPolicy(lcAttentionSession* session, const float* q, const float* k,
+                                              const float* v, float* out, const lcAttentionIoPolicy* policy);
+/* Launch-only repeat of the resident forward (no uploads, no download), then
+ * a stream synchronisation: the attention analogue of
+ * MatMulMetalResidentSession::runBatchSyncCachedNoDownload (ops.hpp:1371-1373). */
+lcError_t lcAttentionSessionRunCached(lcAttentionSession* session, size_t repeat_count);
+
+/* --- matmul ------------------------------------------------------------------ */
+
+/* MatMulIoPolicy (reference include/lightning_core/core/ops/policy.hpp:8-13). */
+typedef struct lcMatMulIoPolicy {
+  int upload_a;
+  int upload_b;
+  int download_out;
+  int synchronize;
+} lcMatMulIoPolicy;
+
+lcMatMulIoPolicy lcMatMulIoPolicyDefault(void);
+
+/* ops::matMul<float> (ops.hpp:195-205): host row-major fp32 A[M,K], B[K,N], C[M,N]. */
+lcError_t lcMatMul(const float* a, const float* b, float* out, size_t m, size_t k, size_t n, lcDeviceKind device);
+
+/* ops::matMulWithPolicy<float> (ops.hpp:354-459).  Null a/b/out are allowed
+ * when the policy does not upload/download them; then the backend's resident
+ * buffers (last uploaded) are used, as the reference's global Metal context
+ * does (matmul_metal.mm:1836-1937). */
+lcError_t lcMatMulWithPolicy(const float* a, const float* b, float* out, size_t m, size_t k, size_t n,
+                             lcDeviceKind device, const lcMatMulIoPolicy* policy);
+
+/* detail::matMulMetalWithPolicyBatched (matmul_metal.mm:1939-2075 /
+ * ops_backend.hpp:254-265): `repeat_count` launches in one submission. */
+lcError_t lcMatMulWithPolicyBatched(const float* a, const float* b, float* out, size_t m, size_t k, size_t n,
+                                    lcDeviceKind device, const lcMatMulIoPolicy* policy, size_t repeat_count);
+
+/* matMulMetalResetTuning (ops_backend.hpp:295): clears the gfx950 tune cache. */
+lcError_t lcMatMulResetTuning(void);
+
+/* MatMulMetalResidentSession<T> (ops.hpp:1339-1379), with session-owned
+ * device buffers and a compute dtype (fp32 host data is rounded to bf16/fp16
+ * once at upload, like the reference's fp16 resident batch path,
+ * matmul_metal.mm:1421-1524).  Output is fp32. */
+typedef struct lcMatMulResidentSession lcMatMulResidentSession;
+
+lcError_t lcMatMulResidentSessionCreate(size_t m, size_t k, size_t n, lcDataType compute_dtype,
+                                        lcMatMulResidentSession** out);
+lcError_t lcMatMulResidentSessionDestroy(lcMatMulResidentSession* s);
+lcError_t lcMatMulResidentSessionStart(lcMatMulResidentSession* s, const float* a, const float* b, float* out);  /* :1347 */
+lcError_t lcMatMulResidentSessionRun(lcMatMulResidentSession* s, const float* a, const float* b, float* out);    /* :1351 */
+lcError_t lcMatMulResidentSessionFinish(lcMatMulResidentSession* s, const float* a, const float* b, float* out); /* :1355 */
+lcError_t lcMatMulResidentSessionSync(lcMatMulResidentSession* s, const float* a, const float* b, float* out);   /* :1359 */
+lcError_t lcMatMulResidentSessionRunBatchSync(lcMatMulResidentSession* s, const float* a, const float* b,
+                                              float* out, size_t repeat_count);                                  /* :1363 */
+lcError_t lcMatMulResidentSessionRunBatchSyncNoDownload(lcMatMulResidentSession* s, const float* a,
+                                                        const float* b, float* out, size_t repeat_count);        /* :1367 */
+lcError_t lcMatMulResidentSessionRunBatchSyncCachedNoDownload(lcMatMulResidentSession* s, size_t repeat_count); /* :1371 */
+
+/* --- conv2d and the integrated conv -> attention pipeline -------------------- */
+
+/* ops::conv2dNchw<float> (ops.hpp:855-1213): x [B,C,H,W], w [OC,C,KH,KW],
+ * bias [OC] or NULL, out [B,OC,OH,OW]; implicit GEMM on the GPU with the
+ * bias / ReLU epilogue fused. */
+lcError_t lcConv2dNchw(const float* x, const float* w, const float* bias, float* out, size_t batch,
+                       size_t in_channels, size_t in_h, size_t in_w, size_t out_channels, size_t kernel_h,
+                       size_t kernel_w, size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w,
+                       lcDeviceKind device, int apply_relu);
+
+/* api.conv_attention_torchstrong_nchw_into (bind_integrated.cpp:614-730,
+ * eager mode): conv2d + ReLU, Q/K/V = consecutive seq_len*head_dim slices of
+ * the flat NCHW output (repeated when short, QkvPackRepeat), single-head
+ * non-causal attention; out [seq_len, head_dim].  All stages stay on the GPU. */
+lcError_t lcConvAttentionTorchstrongNchw(const float* x, const float* w, const float* bias, float* out,
+                                         size_t batch, size_t in_channels, size_t in_h, size_t in_w,
+                                         size_t out_channels, size_t kernel_h, size_t kernel_w, size_t seq_len,
+                                         size_t head_dim, size_t stride_h, size_t stride_w, size_t pad_h,
+                                         size_t pad_w, lcDeviceKind device);
+
+/* ViT-style block (new composition of the reference's conv2dNchw, matMul and
+ * attentionForward): patch-embed conv (kernel = stride = patch, no padding,
+ * no bias) + ReLU -> tokens [B, T, E] -> QKV = tokens . w_qkv [E, 3E] split in
+ * timm (B, T, 3, H, Dh) order -> per-head non-causal attention -> concat ->
+ * . w_o [E, E].  x [B, C, H, W], w_conv [E, C, P, P], out [B, T, E] fp32. */
+typedef struct lcVitBlockConfig {
+  size_t batch;
+  size_t in_channels;
+  size_t image_h;
+  size_t image_w;
+  size_t patch;
+  size_t embed;
+  size_t heads;
+  lcDataType compute_dtype;
+} lcVitBlockConfig;
+
+typedef struct lcVitBlockSession lcVitBlockSession;
+
+lcError_t lcVitBlockSessionCreate(const lcVitBlockConfig* cfg, lcDeviceKind device, lcVitBlockSession** out);
+lcError_t lcVitBlockSessionDestroy(lcVitBlockSession* s);
+/* Uploads (and converts) the weights; they stay resident. */
+lcError_t lcVitBlockSessionSetWeights(lcVitBlockSession* s, const float* w_conv, const float* w_qkv,
+                                      const float* w_o);
+/* One forward: x uploaded when non-NULL (else the resident input is reused),
+ * out downloaded when non-NULL; synchronises when out is non-NULL. */
+lcError_t lcVitBlockSessionForward(lcVitBlockSession* s, const float* x, float* out);
+/* Launch-only repeat over the resident input, then a stream synchronisation. */
+lcError_t lcVitBlockSessionRunCached(lcVitBlockSession* s, size_t repeat_count);
+
+lcError_t lcVitBlockForward(const float* x, const float* w_conv, const float* w_qkv, const float* w_o, float* out,
+                            const lcVitBlockConfig* cfg, lcDeviceKind device);
+
+/* --- device info and timing on the backend stream ---------------------------- */
+
+typedef struct lcHipDeviceInfo {
+  char name[128];
+  char gcn_arch[64];
+  int compute_units;
+  int max_clock_khz;
+  size_t total_memory_bytes;
+  size_t l2_cache_bytes;
+} lcHipDeviceInfo;
+
+lcError_t lcHipGetDeviceInfo(lcHipDeviceInfo* out);
+
+/* HIP events recorded on the backend stream (the stream every kernel of this
+ * library is launched on); Stop synchronises on the stop event and returns
+ * the elapsed milliseconds. */
+typedef struct lcHipTimer lcHipTimer;
+lcError_t lcHipTimerCreate(lcHipTimer** out);
+lcError_t lcHipTimerDestroy(lcHipTimer* t);
+lcError_t lcHipTimerStart(lcHipTimer* t);
+lcError_t lcHipTimerStop(lcHipTimer* t, float* elapsed_ms);
+
+/* Saves / loads the gfx950 tune cache (#lc_tune_cache,matmul,2 CSV). */
+lcError_t lcHipTuneCacheSave(const char* path);
+lcError_t lcHipTuneCacheLoad(const char* path);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LIGHTNING_CORE_HIP_H */

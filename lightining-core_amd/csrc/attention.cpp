@@ -1,0 +1,365 @@
+// attention.cpp -- attention front-end for the "hip" device.
+//
+// Mirrors lightning_core::attentionForwardWithPolicy (reference
+// src/attention.cpp:137-201) and AttentionSession (:247-283):
+//   * validation: null q/k/v/out or zero dims -> kInvalidValue (:146-148);
+//   * workload hint S*S*D (per head) in the op_dispatch trace (:149);
+//   * postprocess out = relu?(out*scale + bias), identity skipped (:41-60);
+//   * sessions default to synchronize = false, loss_every = 0 (:247-254);
+//   * a download always synchronises (the host reads the result).
+// The reference's CPU paths (device cpu, the one-shot CPU crossover and the
+// kNotSupported -> CPU fallback) belong to the reference's own dispatcher; in
+// this library a request that the HIP kernels cannot serve returns an error.
+#include <cmath>
+#include <cstring>
+#include <memory>
+
+#include "ops_internal.hpp"
+
+namespace lchip {
+
+Status requireHip(lcDeviceKind device, const char* op, HipContext** ctx_out) {
+  if (!validDevice(device)) {
+    return fail(Status::kInvalidValue, std::string(op) + ": unknown device");
+  }
+  if (device != LC_DEVICE_HIP) {
+    return fail(Status::kNotSupported, std::string(op) +
+                                           ": this library implements the 'hip' device only; cpu/cuda/metal compute "
+                                           "is served by the reference backends");
+  }
+  Status st = Status::kSuccess;
+  HipContext* ctx = hipContext(&st);
+  if (ctx == nullptr) {
+    return st;
+  }
+  *ctx_out = ctx;
+  return Status::kSuccess;
+}
+
+namespace {
+
+Status uploadAttnTensor(HipContext* ctx, AttnResident& res, const AttnShape& sh, const float* host, DeviceBuffer& dst,
+                        bool transpose) {
+  const std::size_t n = sh.elems();
+  if (!isHalf(sh.dtype)) {
+    LC_TRY(dst.ensure(n * sizeof(float)));
+    return upload(ctx, dst.get(), host, n * sizeof(float));
+  }
+  const std::size_t s_pad = sh.sPad();
+  LC_TRY(res.stage.ensure(n * sizeof(float)));
+  LC_TRY(dst.ensure(sh.bh() * s_pad * sh.head_dim * sizeof(uint16_t)));
+  LC_TRY(upload(ctx, res.stage.get(), host, n * sizeof(float)));
+  const int S = static_cast<int>(sh.seq_len);
+  const int D = static_cast<int>(sh.head_dim);
+  const int bh = static_cast<int>(sh.bh());
+  hipError_t e;
+  if (!transpose) {
+    e = kern::convertPad(res.stage.as<float>(), dst.as<uint16_t>(), bh, S, D, D, static_cast<int>(s_pad), D,
+                         sh.seq_len * sh.head_dim, s_pad * sh.head_dim, halfOf(sh.dtype), ctx->stream);
+  } else {
+    e = kern::convertTransposePad(res.stage.as<float>(), dst.as<uint16_t>(), bh, S, D, D, static_cast<int>(s_pad), D,
+                                  sh.seq_len * sh.head_dim, s_pad * sh.head_dim, halfOf(sh.dtype), ctx->stream);
+  }
+  if (e != hipSuccess) {
+    return failHip(e, "attention upload conversion");
+  }
+  return Status::kSuccess;
+}
+
+bool sameShape(const AttnShape& a, const AttnShape& b) {
+  return a.batch == b.batch && a.heads == b.heads && a.seq_len == b.seq_len && a.head_dim == b.head_dim &&
+         a.dtype == b.dtype;
+}
+
+bool postIsIdentity(const lcAttentionIoPolicy& p) {
+  return p.output_scale == 1.0f && p.output_bias == 0.0f && !p.output_relu;
+}
+
+}  // namespace
+
+Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnShape& sh, const float* q,
+                                const float* k, const float* v, float* out, const lcAttentionIoPolicy& policy,
+                                std::size_t repeat) {
+  if (sh.seq_len == 0 || sh.head_dim == 0 || sh.bh() == 0) {
+    return fail(Status::kInvalidValue, "attention: zero dimension");
+  }
+  if ((policy.upload_q && q == nullptr) || (policy.upload_k && k == nullptr) || (policy.upload_v && v == nullptr) ||
+      (policy.download_out && out == nullptr)) {
+    return fail(Status::kInvalidValue, "attention: null pointer required by the io policy");
+  }
+  if (isHalf(sh.dtype) && sh.head_dim != 64 && sh.head_dim != 128) {
+    return fail(Status::kNotSupported, "attention: 16-bit path supports head_dim 64 or 128");
+  }
+  if (!isHalf(sh.dtype) && sh.head_dim > 256) {
+    return fail(Status::kNotSupported, "attention: fp32 path supports head_dim <= 256");
+  }
+  if (sh.seq_len > (1u << 24) || sh.bh() > 65535u * 64u) {
+    return fail(Status::kNotSupported, "attention: shape too large");
+  }
+  if (!sameShape(res.shape, sh)) {
+    res.has_q = res.has_k = res.has_v = res.has_out = false;
+    res.shape = sh;
+  }
+  if ((!policy.upload_q && !res.has_q) || (!policy.upload_k && !res.has_k) || (!policy.upload_v && !res.has_v)) {
+    return fail(Status::kInvalidValue, "attention: no resident input for a tensor the policy does not upload");
+  }
+
+  const bool half = isHalf(sh.dtype);
+  if (policy.upload_q) {
+    LC_TRY(uploadAttnTensor(ctx, res, sh, q, res.q, false));
+    res.has_q = true;
+  }
+  if (policy.upload_k) {
+    LC_TRY(uploadAttnTensor(ctx, res, sh, k, res.k, false));
+    res.has_k = true;
+  }
+  if (policy.upload_v) {
+    LC_TRY(uploadAttnTensor(ctx, res, sh, v, res.v, half));
+    res.has_v = true;
+  }
+  const std::size_t n = sh.elems();
+  LC_TRY(res.out.ensure(n * sizeof(float)));
+
+  const int S = static_cast<int>(sh.seq_len);
+  const int D = static_cast<int>(sh.head_dim);
+  const int bh = static_cast<int>(sh.bh());
+  const std::size_t hint = sh.seq_len * sh.seq_len * sh.head_dim;
+  for (std::size_t r = 0; r < repeat; ++r) {
+    traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, hint);
+    hipError_t e;
+    if (!half) {
+      e = kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(), bh, S, D,
+                             sh.causal, policy.output_scale, policy.output_bias, policy.output_relu, ctx->stream);
+    } else {
+      e = kern::attentionHalf(res.q.as<uint16_t>(), res.k.as<uint16_t>(), res.v.as<uint16_t>(), res.out.as<float>(),
+                              nullptr, static_cast<int>(sh.heads), bh, S, static_cast<int>(sh.sPad()), D, sh.causal,
+                              halfOf(sh.dtype), ctx->stream);
+      if (e == hipSuccess && !postIsIdentity(policy)) {
+        e = kern::postprocessF32(res.out.as<float>(), n, policy.output_scale, policy.output_bias, policy.output_relu,
+                                 ctx->stream);
+      }
+    }
+    if (e != hipSuccess) {
+      return failHip(e, "attention kernel launch");
+    }
+  }
+  res.has_out = true;
+  if (policy.download_out) {
+    LC_TRY(download(ctx, out, res.out.get(), n * sizeof(float)));
+  }
+  if (policy.download_out || policy.synchronize) {
+    LC_TRY(syncStream(ctx));
+  }
+  return Status::kSuccess;
+}
+
+namespace {
+
+AttnResident& globalAttnResident() {
+  static AttnResident* r = new AttnResident();  // process lifetime, like the reference's global context
+  return *r;
+}
+
+Status attentionOneShot(const float* q, const float* k, const float* v, float* out, const AttnShape& sh,
+                        lcDeviceKind device, const lcAttentionIoPolicy* policy_in) {
+  if (q == nullptr || k == nullptr || v == nullptr || out == nullptr || sh.seq_len == 0 || sh.head_dim == 0 ||
+      sh.bh() == 0) {
+    return fail(Status::kInvalidValue, "attention: null pointer or zero dimension");
+  }
+  if (!validDtype(sh.dtype)) {
+    return fail(Status::kInvalidValue, "attention: unknown compute dtype");
+  }
+  HipContext* ctx = nullptr;
+  LC_TRY(requireHip(device, "attention", &ctx));
+  const lcAttentionIoPolicy policy = policy_in ? *policy_in : lcAttentionIoPolicyDefault();
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  return attentionForwardResident(ctx, globalAttnResident(), sh, q, k, v, out, policy, 1);
+}
+
+}  // namespace
+}  // namespace lchip
+
+using namespace lchip;
+
+struct lcAttentionSession {
+  AttnShape shape;
+  lcDeviceKind device = LC_DEVICE_HIP;
+  lcAttentionIoPolicy default_policy{};
+  AttnResident res;
+};
+
+extern "C" {
+
+lcAttentionIoPolicy lcAttentionIoPolicyDefault(void) {
+  lcAttentionIoPolicy p{};
+  p.upload_q = p.upload_k = p.upload_v = p.upload_target = 1;
+  p.download_out = p.download_v = 1;
+  p.synchronize = 1;
+  p.loss_every = 1;
+  p.output_scale = 1.0f;
+  p.output_bias = 0.0f;
+  p.output_relu = 0;
+  return p;
+}
+
+const char* lcAttentionImplementationName(lcDeviceKind device) {
+  if (device == LC_DEVICE_HIP && hipAvailable()) {
+    return "custom-hip-mfma-flash";
+  }
+  return "unavailable";
+}
+
+lcError_t lcAttentionForward(const float* q, const float* k, const float* v, float* out, const lcAttentionConfig* cfg,
+                             lcDeviceKind device) {
+  return lcAttentionForwardWithPolicy(q, k, v, out, cfg, device, nullptr);
+}
+
+lcError_t lcAttentionForwardWithPolicy(const float* q, const float* k, const float* v, float* out,
+                                       const lcAttentionConfig* cfg, lcDeviceKind device,
+                                       const lcAttentionIoPolicy* policy) {
+  if (cfg == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "attention: null config"));
+  }
+  AttnShape sh;
+  sh.seq_len = cfg->seq_len;
+  sh.head_dim = cfg->head_dim;
+  sh.causal = cfg->causal != 0;
+  return toLc(attentionOneShot(q, k, v, out, sh, device, policy));
+}
+
+lcError_t lcAttentionForwardBatched(const float* q, const float* k, const float* v, float* out,
+                                    const lcAttentionBatchedConfig* cfg, lcDeviceKind device,
+                                    const lcAttentionIoPolicy* policy) {
+  if (cfg == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "attention: null config"));
+  }
+  AttnShape sh;
+  sh.batch = cfg->batch;
+  sh.heads = cfg->heads;
+  sh.seq_len = cfg->seq_len;
+  sh.head_dim = cfg->head_dim;
+  sh.causal = cfg->causal != 0;
+  sh.dtype = cfg->compute_dtype;
+  return toLc(attentionOneShot(q, k, v, out, sh, device, policy));
+}
+
+static lcError_t createSession(const AttnShape& sh, lcDeviceKind device, lcAttentionSession** out) {
+  if (out == nullptr || sh.seq_len == 0 || sh.head_dim == 0 || sh.bh() == 0 || !validDtype(sh.dtype)) {
+    return toLc(fail(Status::kInvalidValue, "attention session: invalid arguments"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(device, "attention session", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  auto* s = new lcAttentionSession();
+  s->shape = sh;
+  s->device = device;
+  s->default_policy = lcAttentionIoPolicyDefault();
+  // Session defaults target repeated execution (reference src/attention.cpp:249-253).
+  s->default_policy.synchronize = 0;
+  s->default_policy.loss_every = 0;
+  s->res.shape = sh;
+  *out = s;
+  return LC_SUCCESS;
+}
+
+lcError_t lcAttentionSessionCreate(const lcAttentionConfig* cfg, lcDeviceKind device, lcAttentionSession** out) {
+  if (cfg == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "attention session: null config"));
+  }
+  AttnShape sh;
+  sh.seq_len = cfg->seq_len;
+  sh.head_dim = cfg->head_dim;
+  sh.causal = cfg->causal != 0;
+  return createSession(sh, device, out);
+}
+
+lcError_t lcAttentionSessionCreateBatched(const lcAttentionBatchedConfig* cfg, lcDeviceKind device,
+                                          lcAttentionSession** out) {
+  if (cfg == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "attention session: null config"));
+  }
+  AttnShape sh;
+  sh.batch = cfg->batch;
+  sh.heads = cfg->heads;
+  sh.seq_len = cfg->seq_len;
+  sh.head_dim = cfg->head_dim;
+  sh.causal = cfg->causal != 0;
+  sh.dtype = cfg->compute_dtype;
+  return createSession(sh, device, out);
+}
+
+lcError_t lcAttentionSessionDestroy(lcAttentionSession* session) {
+  if (session == nullptr) {
+    return LC_INVALID_VALUE;
+  }
+  Status st = Status::kSuccess;
+  HipContext* ctx = hipContext(&st);
+  if (ctx != nullptr) {
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipStreamSynchronize(ctx->stream);  // no kernel may still use the buffers
+    delete session;
+  } else {
+    delete session;
+  }
+  return LC_SUCCESS;
+}
+
+lcError_t lcAttentionSessionSetDefaultPolicy(lcAttentionSession* session, const lcAttentionIoPolicy* policy) {
+  if (session == nullptr || policy == nullptr) {
+    return LC_INVALID_VALUE;
+  }
+  session->default_policy = *policy;
+  return LC_SUCCESS;
+}
+
+lcError_t lcAttentionSessionGetDefaultPolicy(const lcAttentionSession* session, lcAttentionIoPolicy* out) {
+  if (session == nullptr || out == nullptr) {
+    return LC_INVALID_VALUE;
+  }
+  *out = session->default_policy;
+  return LC_SUCCESS;
+}
+
+lcError_t lcAttentionSessionForwardWithPolicy(lcAttentionSession* session, const float* q, const float* k,
+                                              const float* v, float* out, const lcAttentionIoPolicy* policy) {
+  if (session == nullptr || policy == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "attention session: null session or policy"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(session->device, "attention session", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  return toLc(attentionForwardResident(ctx, session->res, session->shape, q, k, v, out, *policy, 1));
+}
+
+lcError_t lcAttentionSessionForward(lcAttentionSession* session, const float* q, const float* k, const float* v,
+                                    float* out) {
+  if (session == nullptr) {
+    return LC_INVALID_VALUE;
+  }
+  return lcAttentionSessionForwardWithPolicy(session, q, k, v, out, &session->default_policy);
+}
+
+lcError_t lcAttentionSessionRunCached(lcAttentionSession* session, size_t repeat_count) {
+  if (session == nullptr || repeat_count == 0) {
+    return toLc(fail(Status::kInvalidValue, "attention session: null session or zero repeat"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(session->device, "attention session", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  lcAttentionIoPolicy p = session->default_policy;
+  p.upload_q = p.upload_k = p.upload_v = 0;
+  p.download_out = 0;
+  p.synchronize = 1;
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  return toLc(attentionForwardResident(ctx, session->res, session->shape, nullptr, nullptr, nullptr, nullptr, p,
+                                       repeat_count));
+}
+
+}  // extern "C"

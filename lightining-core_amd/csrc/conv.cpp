@@ -1,0 +1,469 @@
+// conv.cpp -- conv2d, the integrated conv -> attention pipeline and the
+// ViT-style block for the "hip" device.
+//
+//  * lcConv2dNchw mirrors ops::conv2dNchw<float> (reference core/ops.hpp:
+//    855-1213): same validation (:873-884) and geometry (:886-892); the GPU
+//    form is im2col + fp32 MFMA GEMM with the bias / ReLU / NCHW scatter fused
+//    into the GEMM epilogue (the reference runs them as separate CPU loops).
+//  * lcConvAttentionTorchstrongNchw mirrors convAttentionTorchstrongNchwInto-
+//    Direct (python/bindings/bind_integrated.cpp:614-730): conv + ReLU, Q/K/V
+//    as consecutive S*D slices of the flat NCHW output, repeated when short
+//    (QkvPackRepeat :709-729), then single-head attention.  Every stage stays
+//    in device memory (the reference round-trips through host vectors).
+//  * The ViT block chains four kernels on one stream with the re-layouts in
+//    the epilogues: implicit-GEMM patch-embed conv (+ReLU) writing tokens
+//    [B*T, E]; QKV GEMM writing head-major Q/K and transposed V; flash
+//    attention writing heads concatenated [B*T, E]; output projection.
+#include <cstring>
+#include <map>
+#include <string>
+#include <tuple>
+
+#include "ops_internal.hpp"
+
+namespace lchip {
+namespace {
+
+struct ConvResident {
+  DeviceBuffer x, w, bias, cols, out, packed, attn_out;
+};
+
+ConvResident& globalConv() {
+  static ConvResident* r = new ConvResident();  // process lifetime
+  return *r;
+}
+
+struct ConvGeom {
+  std::size_t batch, in_c, in_h, in_w, out_c, kh, kw, sh, sw, ph, pw, out_h, out_w;
+  std::size_t rows() const { return batch * out_h * out_w; }
+  std::size_t kin() const { return in_c * kh * kw; }
+  std::size_t outSize() const { return batch * out_c * out_h * out_w; }
+};
+
+Status makeGeom(std::size_t batch, std::size_t in_c, std::size_t in_h, std::size_t in_w, std::size_t out_c,
+                std::size_t kh, std::size_t kw, std::size_t sh, std::size_t sw, std::size_t ph, std::size_t pw,
+                ConvGeom* g) {
+  if (batch == 0 || in_c == 0 || in_h == 0 || in_w == 0 || out_c == 0 || kh == 0 || kw == 0 || sh == 0 || sw == 0) {
+    return fail(Status::kInvalidValue, "conv2d: zero dimension or stride");
+  }
+  if (in_h + 2 * ph < kh || in_w + 2 * pw < kw) {
+    return fail(Status::kInvalidValue, "conv2d: kernel larger than padded input");
+  }
+  g->batch = batch;
+  g->in_c = in_c;
+  g->in_h = in_h;
+  g->in_w = in_w;
+  g->out_c = out_c;
+  g->kh = kh;
+  g->kw = kw;
+  g->sh = sh;
+  g->sw = sw;
+  g->ph = ph;
+  g->pw = pw;
+  g->out_h = (in_h + 2 * ph - kh) / sh + 1;
+  g->out_w = (in_w + 2 * pw - kw) / sw + 1;
+  if (g->rows() * g->kin() > (std::size_t(1) << 31) || g->outSize() > (std::size_t(1) << 31)) {
+    return fail(Status::kNotSupported, "conv2d: shape too large");
+  }
+  return Status::kSuccess;
+}
+
+// Uploads x / w / bias and leaves relu?(conv + bias) in r.out (NCHW, fp32).
+Status convForwardDevice(HipContext* ctx, ConvResident& r, const ConvGeom& g, const float* x, const float* w,
+                         const float* bias, bool relu) {
+  const std::size_t xs = g.batch * g.in_c * g.in_h * g.in_w;
+  const std::size_t ws = g.out_c * g.kin();
+  LC_TRY(r.x.ensure(xs * sizeof(float)));
+  LC_TRY(r.w.ensure(ws * sizeof(float)));
+  LC_TRY(upload(ctx, r.x.get(), x, xs * sizeof(float)));
+  LC_TRY(upload(ctx, r.w.get(), w, ws * sizeof(float)));
+  const float* dbias = nullptr;
+  if (bias != nullptr) {
+    LC_TRY(r.bias.ensure(g.out_c * sizeof(float)));
+    LC_TRY(upload(ctx, r.bias.get(), bias, g.out_c * sizeof(float)));
+    dbias = r.bias.as<float>();
+  }
+  LC_TRY(r.cols.ensure(g.rows() * g.kin() * sizeof(float)));
+  LC_TRY(r.out.ensure(g.outSize() * sizeof(float)));
+  traceOpDispatch(TraceOp::kConv2dNchw, Device::kHIP, Device::kHIP, false,
+                  g.rows() * g.out_c * g.kin());
+  hipError_t e = kern::im2colF32(r.x.as<float>(), r.cols.as<float>(), static_cast<int>(g.batch),
+                                 static_cast<int>(g.in_c), static_cast<int>(g.in_h), static_cast<int>(g.in_w),
+                                 static_cast<int>(g.kh), static_cast<int>(g.kw), static_cast<int>(g.sh),
+                                 static_cast<int>(g.sw), static_cast<int>(g.ph), static_cast<int>(g.pw),
+                                 static_cast<int>(g.out_h), static_cast<int>(g.out_w), ctx->stream);
+  if (e == hipSuccess) {
+    e = kern::gemmF32ConvNchw(r.cols.as<float>(), r.w.as<float>(), r.out.as<float>(), static_cast<int>(g.rows()),
+                              static_cast<int>(g.out_c), static_cast<int>(g.kin()), dbias, relu ? 1 : 0,
+                              static_cast<int>(g.out_h * g.out_w), ctx->stream);
+  }
+  return e == hipSuccess ? Status::kSuccess : failHip(e, "conv2d kernel launch");
+}
+
+}  // namespace
+}  // namespace lchip
+
+using namespace lchip;
+
+// ---------------------------------------------------------------------------
+// ViT block session
+// ---------------------------------------------------------------------------
+struct lcVitBlockSession {
+  lcVitBlockConfig cfg{};
+  lcDeviceKind device = LC_DEVICE_HIP;
+  std::size_t gh = 0, gw = 0, T = 0, M = 0, Mp = 0, K = 0, Dh = 0, S_pad = 0;
+  DeviceBuffer stage, x16, wconv16, wqkv_t16, wo_t16, tokens16, q16, k16, vt16, attn16, out;
+  bool has_w = false, has_x = false;
+};
+
+namespace {
+
+Status vitValidate(const lcVitBlockConfig& c) {
+  if (c.batch == 0 || c.in_channels == 0 || c.patch == 0 || c.embed == 0 || c.heads == 0 || c.image_h < c.patch ||
+      c.image_w < c.patch) {
+    return fail(Status::kInvalidValue, "vit block: zero dimension or image smaller than the patch");
+  }
+  if (!isHalf(c.compute_dtype)) {
+    return fail(Status::kNotSupported, "vit block: compute dtype must be bf16 or f16");
+  }
+  const std::size_t dh = c.embed / c.heads;
+  if (c.embed % c.heads != 0 || (dh != 64 && dh != 128)) {
+    return fail(Status::kNotSupported, "vit block: embed / heads must be 64 or 128");
+  }
+  if (c.patch % 8 != 0 || c.image_w % 8 != 0 || (c.in_channels * c.patch * c.patch) % kern::kHalfGemmBK != 0 ||
+      c.embed % kern::kHalfGemmBK != 0) {
+    return fail(Status::kNotSupported,
+                "vit block: needs patch % 8 == 0, image_w % 8 == 0, C*P*P % 64 == 0 and embed % 64 == 0");
+  }
+  return Status::kSuccess;
+}
+
+Status vitForwardDevice(HipContext* ctx, lcVitBlockSession* s) {
+  const auto& c = s->cfg;
+  const kern::Half ht = halfOf(c.compute_dtype);
+  const int B = static_cast<int>(c.batch);
+  const int E = static_cast<int>(c.embed);
+  const int H = static_cast<int>(c.heads);
+  const int T = static_cast<int>(s->T);
+  const int M = static_cast<int>(s->M);
+  traceOpDispatch(TraceOp::kConv2dNchw, Device::kHIP, Device::kHIP, false, s->M * c.embed * s->K);
+  hipError_t e = kern::patchEmbedGemm(s->x16.as<uint16_t>(), s->wconv16.as<uint16_t>(), s->tokens16.as<uint16_t>(), B,
+                                      static_cast<int>(c.in_channels), static_cast<int>(c.image_h),
+                                      static_cast<int>(c.image_w), static_cast<int>(c.patch), E, ht, ctx->stream);
+  if (e != hipSuccess) {
+    return failHip(e, "vit patch-embed launch");
+  }
+  traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, s->M * c.embed * 3 * c.embed);
+  e = kern::qkvProjectGemm(s->tokens16.as<uint16_t>(), s->wqkv_t16.as<uint16_t>(), s->q16.as<uint16_t>(),
+                           s->k16.as<uint16_t>(), s->vt16.as<uint16_t>(), B, T, E, H, static_cast<int>(s->S_pad), ht,
+                           ctx->stream);
+  if (e != hipSuccess) {
+    return failHip(e, "vit qkv launch");
+  }
+  traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, s->T * s->T * s->Dh);
+  e = kern::attentionHalf(s->q16.as<uint16_t>(), s->k16.as<uint16_t>(), s->vt16.as<uint16_t>(), nullptr,
+                          s->attn16.as<uint16_t>(), H, B * H, T, static_cast<int>(s->S_pad), static_cast<int>(s->Dh),
+                          false, ht, ctx->stream);
+  if (e != hipSuccess) {
+    return failHip(e, "vit attention launch");
+  }
+  traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, s->M * c.embed * c.embed);
+  e = kern::gemmHalfTN(s->attn16.as<uint16_t>(), s->wo_t16.as<uint16_t>(), s->out.as<float>(), M, E, E, E, E, E, ht,
+                       ctx->stream);
+  return e == hipSuccess ? Status::kSuccess : failHip(e, "vit out-projection launch");
+}
+
+Status vitUploadX(HipContext* ctx, lcVitBlockSession* s, const float* x) {
+  const auto& c = s->cfg;
+  const std::size_t n = c.batch * c.in_channels * c.image_h * c.image_w;
+  LC_TRY(upload(ctx, s->stage.get(), x, n * sizeof(float)));
+  const hipError_t e = kern::convertPad(s->stage.as<float>(), s->x16.as<uint16_t>(), 1,
+                                        static_cast<int>(c.batch * c.in_channels * c.image_h),
+                                        static_cast<int>(c.image_w), c.image_w,
+                                        static_cast<int>(c.batch * c.in_channels * c.image_h),
+                                        static_cast<int>(c.image_w), 0, 0, halfOf(c.compute_dtype), ctx->stream);
+  if (e != hipSuccess) {
+    return failHip(e, "vit input conversion");
+  }
+  s->has_x = true;
+  return Status::kSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+lcError_t lcConv2dNchw(const float* x, const float* w, const float* bias, float* out, size_t batch, size_t in_channels,
+                       size_t in_h, size_t in_w, size_t out_channels, size_t kernel_h, size_t kernel_w,
+                       size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w, lcDeviceKind device,
+                       int apply_relu) {
+  if (x == nullptr || w == nullptr || out == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "conv2d: null pointer"));
+  }
+  ConvGeom g{};
+  Status st = makeGeom(batch, in_channels, in_h, in_w, out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                       pad_w, &g);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  HipContext* ctx = nullptr;
+  st = requireHip(device, "conv2d", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  ConvResident& r = globalConv();
+  st = convForwardDevice(ctx, r, g, x, w, bias, apply_relu != 0);
+  if (st == Status::kSuccess) {
+    st = download(ctx, out, r.out.get(), g.outSize() * sizeof(float));
+  }
+  if (st == Status::kSuccess) {
+    st = syncStream(ctx);
+  }
+  return toLc(st);
+}
+
+lcError_t lcConvAttentionTorchstrongNchw(const float* x, const float* w, const float* bias, float* out, size_t batch,
+                                         size_t in_channels, size_t in_h, size_t in_w, size_t out_channels,
+                                         size_t kernel_h, size_t kernel_w, size_t seq_len, size_t head_dim,
+                                         size_t stride_h, size_t stride_w, size_t pad_h, size_t pad_w,
+                                         lcDeviceKind device) {
+  if (x == nullptr || w == nullptr || out == nullptr || seq_len == 0 || head_dim == 0) {
+    return toLc(fail(Status::kInvalidValue, "conv_attention: null pointer or zero seq_len/head_dim"));
+  }
+  if (head_dim > 256) {
+    return toLc(fail(Status::kNotSupported, "conv_attention: head_dim <= 256"));
+  }
+  ConvGeom g{};
+  Status st = makeGeom(batch, in_channels, in_h, in_w, out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                       pad_w, &g);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  HipContext* ctx = nullptr;
+  st = requireHip(device, "conv_attention", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  ConvResident& r = globalConv();
+  st = convForwardDevice(ctx, r, g, x, w, bias, true);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  const std::size_t need = seq_len * head_dim;
+  const std::size_t total = 3 * need;
+  const float* src = r.out.as<float>();
+  hipError_t e = hipSuccess;
+  if (g.outSize() < total) {
+    st = r.packed.ensure(total * sizeof(float));
+    if (st != Status::kSuccess) {
+      return toLc(st);
+    }
+    e = kern::repeatFillF32(r.out.as<float>(), g.outSize(), r.packed.as<float>(), total, ctx->stream);
+    src = r.packed.as<float>();
+  }
+  st = r.attn_out.ensure(need * sizeof(float));
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  if (e == hipSuccess) {
+    traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, seq_len * seq_len * head_dim);
+    e = kern::attentionF32(src, src + need, src + 2 * need, r.attn_out.as<float>(), 1, static_cast<int>(seq_len),
+                           static_cast<int>(head_dim), false, 1.0f, 0.0f, 0, ctx->stream);
+  }
+  if (e != hipSuccess) {
+    return toLc(failHip(e, "conv_attention launch"));
+  }
+  st = download(ctx, out, r.attn_out.get(), need * sizeof(float));
+  if (st == Status::kSuccess) {
+    st = syncStream(ctx);
+  }
+  return toLc(st);
+}
+
+lcError_t lcVitBlockSessionCreate(const lcVitBlockConfig* cfg, lcDeviceKind device, lcVitBlockSession** out) {
+  if (cfg == nullptr || out == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "vit block: null argument"));
+  }
+  Status st = vitValidate(*cfg);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  HipContext* ctx = nullptr;
+  st = requireHip(device, "vit block", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  auto* s = new lcVitBlockSession();
+  s->cfg = *cfg;
+  s->device = device;
+  const auto& c = *cfg;
+  s->gh = (c.image_h - c.patch) / c.patch + 1;
+  s->gw = (c.image_w - c.patch) / c.patch + 1;
+  s->T = s->gh * s->gw;
+  s->M = c.batch * s->T;
+  s->Mp = roundUp(s->M, kern::kHalfGemmBM);
+  s->K = c.in_channels * c.patch * c.patch;
+  s->Dh = c.embed / c.heads;
+  s->S_pad = roundUp(s->T, kern::kAttnQBlock);
+  const std::size_t E = c.embed;
+  const std::size_t xs = c.batch * c.in_channels * c.image_h * c.image_w;
+  const std::size_t bh = c.batch * c.heads;
+  const std::size_t h2 = sizeof(uint16_t);
+  st = s->stage.ensure(std::max({xs, E * s->K, E * 3 * E}) * sizeof(float));
+  if (st == Status::kSuccess) st = s->x16.ensure(xs * h2);
+  if (st == Status::kSuccess) st = s->wconv16.ensure(roundUp(E, kern::kHalfGemmBN) * s->K * h2, true);
+  if (st == Status::kSuccess) st = s->wqkv_t16.ensure(roundUp(3 * E, kern::kHalfGemmBN) * E * h2, true);
+  if (st == Status::kSuccess) st = s->wo_t16.ensure(roundUp(E, kern::kHalfGemmBN) * E * h2, true);
+  if (st == Status::kSuccess) st = s->tokens16.ensure(s->Mp * E * h2, true);
+  if (st == Status::kSuccess) st = s->q16.ensure(bh * s->S_pad * s->Dh * h2, true);
+  if (st == Status::kSuccess) st = s->k16.ensure(bh * s->S_pad * s->Dh * h2, true);
+  if (st == Status::kSuccess) st = s->vt16.ensure(bh * s->S_pad * s->Dh * h2, true);
+  if (st == Status::kSuccess) st = s->attn16.ensure(s->Mp * E * h2, true);
+  if (st == Status::kSuccess) st = s->out.ensure(s->M * E * sizeof(float));
+  if (st != Status::kSuccess) {
+    delete s;
+    return toLc(st);
+  }
+  *out = s;
+  return LC_SUCCESS;
+}
+
+lcError_t lcVitBlockSessionDestroy(lcVitBlockSession* s) {
+  if (s == nullptr) {
+    return LC_INVALID_VALUE;
+  }
+  Status st = Status::kSuccess;
+  HipContext* ctx = hipContext(&st);
+  if (ctx != nullptr) {
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipStreamSynchronize(ctx->stream);
+  }
+  delete s;
+  return LC_SUCCESS;
+}
+
+lcError_t lcVitBlockSessionSetWeights(lcVitBlockSession* s, const float* w_conv, const float* w_qkv,
+                                      const float* w_o) {
+  if (s == nullptr || w_conv == nullptr || w_qkv == nullptr || w_o == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "vit block: null weights"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(s->device, "vit block", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  const auto& c = s->cfg;
+  const kern::Half ht = halfOf(c.compute_dtype);
+  const int E = static_cast<int>(c.embed);
+  const int K = static_cast<int>(s->K);
+  // w_conv [E, C, P, P] is already Bt-shaped ([N = E, K]).
+  st = upload(ctx, s->stage.get(), w_conv, c.embed * s->K * sizeof(float));
+  hipError_t e = hipSuccess;
+  if (st == Status::kSuccess) {
+    e = kern::convertPad(s->stage.as<float>(), s->wconv16.as<uint16_t>(), 1, E, K, s->K, E, K, 0, 0, ht, ctx->stream);
+  }
+  // w_qkv [E, 3E] -> [3E, E]
+  if (st == Status::kSuccess && e == hipSuccess) {
+    st = upload(ctx, s->stage.get(), w_qkv, c.embed * 3 * c.embed * sizeof(float));
+  }
+  if (st == Status::kSuccess && e == hipSuccess) {
+    e = kern::convertTransposePad(s->stage.as<float>(), s->wqkv_t16.as<uint16_t>(), 1, E, 3 * E, 3 * c.embed, E,
+                                  3 * E, 0, 0, ht, ctx->stream);
+  }
+  // w_o [E, E] -> transposed
+  if (st == Status::kSuccess && e == hipSuccess) {
+    st = upload(ctx, s->stage.get(), w_o, c.embed * c.embed * sizeof(float));
+  }
+  if (st == Status::kSuccess && e == hipSuccess) {
+    e = kern::convertTransposePad(s->stage.as<float>(), s->wo_t16.as<uint16_t>(), 1, E, E, c.embed, E, E, 0, 0, ht,
+                                  ctx->stream);
+  }
+  if (st == Status::kSuccess && e != hipSuccess) {
+    st = failHip(e, "vit weight conversion");
+  }
+  if (st == Status::kSuccess) {
+    st = syncStream(ctx);
+  }
+  if (st == Status::kSuccess) {
+    s->has_w = true;
+  }
+  return toLc(st);
+}
+
+lcError_t lcVitBlockSessionForward(lcVitBlockSession* s, const float* x, float* out) {
+  if (s == nullptr) {
+    return LC_INVALID_VALUE;
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(s->device, "vit block", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  if (!s->has_w) {
+    return toLc(fail(Status::kInvalidValue, "vit block: weights not set"));
+  }
+  if (x != nullptr) {
+    st = vitUploadX(ctx, s, x);
+  } else if (!s->has_x) {
+    st = fail(Status::kInvalidValue, "vit block: no resident input");
+  }
+  if (st == Status::kSuccess) {
+    st = vitForwardDevice(ctx, s);
+  }
+  if (st == Status::kSuccess && out != nullptr) {
+    st = download(ctx, out, s->out.get(), s->M * s->cfg.embed * sizeof(float));
+    if (st == Status::kSuccess) {
+      st = syncStream(ctx);
+    }
+  }
+  return toLc(st);
+}
+
+lcError_t lcVitBlockSessionRunCached(lcVitBlockSession* s, size_t repeat_count) {
+  if (s == nullptr || repeat_count == 0) {
+    return toLc(fail(Status::kInvalidValue, "vit block: null session or zero repeat"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(s->device, "vit block", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  if (!s->has_w || !s->has_x) {
+    return toLc(fail(Status::kInvalidValue, "vit block: weights or input not resident"));
+  }
+  for (size_t i = 0; i < repeat_count && st == Status::kSuccess; ++i) {
+    st = vitForwardDevice(ctx, s);
+  }
+  if (st == Status::kSuccess) {
+    st = syncStream(ctx);
+  }
+  return toLc(st);
+}
+
+lcError_t lcVitBlockForward(const float* x, const float* w_conv, const float* w_qkv, const float* w_o, float* out,
+                            const lcVitBlockConfig* cfg, lcDeviceKind device) {
+  if (x == nullptr || out == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "vit block: null pointer"));
+  }
+  lcVitBlockSession* s = nullptr;
+  lcError_t e = lcVitBlockSessionCreate(cfg, device, &s);
+  if (e != LC_SUCCESS) {
+    return e;
+  }
+  e = lcVitBlockSessionSetWeights(s, w_conv, w_qkv, w_o);
+  if (e == LC_SUCCESS) {
+    e = lcVitBlockSessionForward(s, x, out);
+  }
+  const std::string msg = lastError();
+  lcVitBlockSessionDestroy(s);
+  setLastError(msg);
+  return e;
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// kernels.hpp -- host-side launchers for the gfx950 kernels.  Every launcher
+// enqueues on the given stream and returns the launch status; shapes are
+// validated by the callers (the dispatch layer) before launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace lchip::kern {
+
+enum class Half { kBF16, kF16 };
+
+// Tile geometry the callers pad buffers to.
+constexpr int kHalfGemmBM = 256;  // rows of A a half-GEMM block may read
+constexpr int kHalfGemmBN = 256;  // rows of Bt a half-GEMM block may read
+constexpr int kHalfGemmBK = 64;   // K must be a multiple of this (zero-padded)
+constexpr int kAttnQBlock = 128;  // queries per attention workgroup; S_pad multiple
+
+// ---- fp32 ------------------------------------------------------------------
+// C[M,N] = A[M,K] . B[K,N] (row-major, leading dimensions lda/ldb/ldc), any sizes.
+hipError_t gemmF32(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
+                   hipStream_t stream);
+// out2d = cols[M,K] . Wt^T where Wt is [N,K] (conv weights as stored, OIHW);
+// epilogue adds bias, applies ReLU and scatters to NCHW out[img, n, pix]
+// (m = img*ohw + pix).
+hipError_t gemmF32ConvNchw(const float* cols, const float* Wt, float* out, int M, int N, int K, const float* bias,
+                           int relu, int ohw, hipStream_t stream);
+// cols[row, col] = x[n, c, oy*sh + ky - ph, ox*sw + kx - pw] (0 outside);
+// row = (n*oh + oy)*ow + ox, col = (c*kh + ky)*kw + kx.
+hipError_t im2colF32(const float* x, float* cols, int batch, int C, int H, int W, int kh, int kw, int sh, int sw,
+                     int ph, int pw, int oh, int ow, hipStream_t stream);
+// Fills dst with the first `total` floats of the infinite repetition of src[0:n].
+hipError_t repeatFillF32(const float* src, size_t n, float* dst, size_t total, hipStream_t stream);
+
+// x = relu?(x*scale + bias), in place (the attention output postprocess,
+// reference src/attention.cpp:41-60).
+hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu, hipStream_t stream);
+
+// Attention over `bh` independent [S, D] fp32 problems (head stride S*D),
+// D <= 256.  Output postprocess relu?(o*post_scale + post_bias).
+hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D,
+                        bool causal, float post_scale, float post_bias, int post_relu, hipStream_t stream);
+
+// ---- 16-bit ------------------------------------------------------------------
+// dst[b][r][c] = half(src[b][r][c]) for r < rows, c < cols; 0 up to
+// rows_pad x cols_pad.  src row stride ld_src, batch strides in elements.
+hipError_t convertPad(const float* src, uint16_t* dst, int batch, int rows, int cols, size_t ld_src,
+                      int rows_pad, int cols_pad, size_t src_bstride, size_t dst_bstride, Half t,
+                      hipStream_t stream);
+// dst[b][c][r] = half(src[b][r][c]) (transpose), zero padding to
+// cols_pad x rows_pad.
+hipError_t convertTransposePad(const float* src, uint16_t* dst, int batch, int rows, int cols, size_t ld_src,
+                               int rows_pad, int cols_pad, size_t src_bstride, size_t dst_bstride, Half t,
+                               hipStream_t stream);
+
+// C[M,N] (fp32, ldc) = A[M,K] . Bt[N,K]^T with A, Bt 16-bit row-major (lda,
+// ldb), K a multiple of kHalfGemmBK, A readable up to roundup(M, 256) rows and
+// Bt up to roundup(N, 256) rows.
+hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda, int ldb,
+                      int ldc, Half t, hipStream_t stream);
+// Same GEMM with a 16-bit output (optionally ReLU).
+hipError_t gemmHalfTNHalfOut(const uint16_t* A, const uint16_t* Bt, uint16_t* C, int M, int N, int K, int lda,
+                             int ldb, int ldc, int relu, Half t, hipStream_t stream);
+
+// Patch-embed convolution as implicit GEMM (kernel = stride = P, no padding):
+// tokens[b*T + t, e] = relu(sum_k x[b, c, ty*P+ky, tx*P+kx] * w[e, c, ky, kx])
+// with x 16-bit NCHW [B, C, H, W], Wt = w as [E, C*P*P] 16-bit; tokens 16-bit
+// [roundup(B*T, 256), E].  Requires P % 8 == 0 and (C*P*P) % 64 == 0.
+hipError_t patchEmbedGemm(const uint16_t* x, const uint16_t* Wt, uint16_t* tokens, int B, int C, int H, int W, int P,
+                          int E, Half t, hipStream_t stream);
+// QKV projection for the ViT block: qkv = tokens[M, E] . Wqkv_t[3E, E]^T with
+// the epilogue writing head-major Q, K [B*H, S_pad, Dh] and V transposed
+// Vt [B*H, Dh, S_pad] (16-bit), M = B*T, S = T.
+hipError_t qkvProjectGemm(const uint16_t* tokens, const uint16_t* Wqkv_t, uint16_t* q, uint16_t* k, uint16_t* vt,
+                          int B, int T, int E, int H, int S_pad, Half t, hipStream_t stream);
+
+// Flash attention over `bh` problems: Q, K [bh, S_pad, D], Vt [bh, D, S_pad]
+// (16-bit, zero padded to S_pad = roundup(S, 128)), D in {64, 128}.  Output
+// either fp32 out_f32[bh, S, D] or, when out_heads_concat != nullptr, 16-bit
+// rows out[(b*S + s), h*D + d] of a [B*S, H*D] matrix (heads = H).
+hipError_t attentionHalf(const uint16_t* q, const uint16_t* k, const uint16_t* vt, float* out_f32,
+                         uint16_t* out_heads_concat, int heads, int bh, int S, int S_pad, int D, bool causal, Half t,
+                         hipStream_t stream);
+
+}  // namespace lchip::kern

@@ -1,0 +1,200 @@
+// convert.hip -- layout and precision passes that feed the MFMA kernels.
+//
+// These run once per upload (resident sessions) or once per one-shot call;
+// they are HBM-bound streaming kernels: coalesced reads, 16-byte writes where
+// the layout allows, and an LDS-staged 32x64 tile for the transposing form.
+#include "../kernels.hpp"
+#include "kcommon.hpp"
+
+namespace lchip::k {
+
+template <typename T>
+__global__ __launch_bounds__(256) void convert_pad_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
+                                                          int rows, int cols, size_t ld_src, int rows_pad,
+                                                          int cols_pad, size_t src_bstride, size_t dst_bstride) {
+  const size_t b = blockIdx.z;
+  src += b * src_bstride;
+  dst += b * dst_bstride;
+  // 4 output elements per thread along the (padded) row.
+  const int c4 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  const int r = blockIdx.y;
+  if (c4 >= cols_pad || r >= rows_pad) {
+    return;
+  }
+  uint16_t h[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int c = c4 + j;
+    const float v = (r < rows && c < cols) ? src[static_cast<size_t>(r) * ld_src + c] : 0.0f;
+    h[j] = to_half_bits<T>(v);
+  }
+  uint16_t* out = dst + static_cast<size_t>(r) * cols_pad + c4;
+  if (c4 + 3 < cols_pad && (cols_pad & 3) == 0) {
+    u32x2 w;
+    w[0] = static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+    w[1] = static_cast<uint32_t>(h[2]) | (static_cast<uint32_t>(h[3]) << 16);
+    *reinterpret_cast<u32x2*>(out) = w;
+  } else {
+    for (int j = 0; j < 4 && c4 + j < cols_pad; ++j) {
+      out[j] = h[j];
+    }
+  }
+}
+
+// dst[c][r] = half(src[r][c]); block = 32 (r) x 64 (c) tile.
+template <typename T>
+__global__ __launch_bounds__(256) void convert_transpose_pad_kernel(const float* __restrict__ src,
+                                                                    uint16_t* __restrict__ dst, int rows, int cols,
+                                                                    size_t ld_src, int rows_pad, int cols_pad,
+                                                                    size_t src_bstride, size_t dst_bstride) {
+  __shared__ float tile[64][33];
+  const size_t b = blockIdx.z;
+  src += b * src_bstride;
+  dst += b * dst_bstride;
+  const int r0 = blockIdx.y * 32;
+  const int c0 = blockIdx.x * 64;
+  const int tx = threadIdx.x & 63;
+  const int ty = threadIdx.x >> 6;  // 0..3
+  for (int rr = ty; rr < 32; rr += 4) {
+    const int r = r0 + rr;
+    const int c = c0 + tx;
+    tile[tx][rr] = (r < rows && c < cols) ? src[static_cast<size_t>(r) * ld_src + c] : 0.0f;
+  }
+  __syncthreads();
+  // write: dst row = c (64 of them), 32 consecutive r per row
+  const int lr = threadIdx.x & 31;
+  const int lc = threadIdx.x >> 5;  // 0..7
+  for (int cc = lc; cc < 64; cc += 8) {
+    const int c = c0 + cc;
+    const int r = r0 + lr;
+    if (c < cols_pad && r < rows_pad) {
+      dst[static_cast<size_t>(c) * rows_pad + r] = to_half_bits<T>(tile[cc][lr]);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void im2col_f32_kernel(const float* __restrict__ x, float* __restrict__ cols,
+                                                         int C, int H, int W, int kh, int kw, int sh, int sw, int ph,
+                                                         int pw, int oh, int ow, size_t total) {
+  const int K = C * kh * kw;
+  for (size_t idx = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; idx < total;
+       idx += static_cast<size_t>(gridDim.x) * 256) {
+    const size_t row = idx / K;
+    const int col = static_cast<int>(idx - row * K);
+    const int c = col / (kh * kw);
+    const int rr = col - c * kh * kw;
+    const int ky = rr / kw;
+    const int kx = rr - ky * kw;
+    const int n = static_cast<int>(row / (static_cast<size_t>(oh) * ow));
+    const int pix = static_cast<int>(row - static_cast<size_t>(n) * oh * ow);
+    const int oy = pix / ow;
+    const int ox = pix - oy * ow;
+    const int y = oy * sh + ky - ph;
+    const int xx = ox * sw + kx - pw;
+    float v = 0.0f;
+    if (y >= 0 && y < H && xx >= 0 && xx < W) {
+      v = x[((static_cast<size_t>(n) * C + c) * H + y) * W + xx];
+    }
+    cols[idx] = v;
+  }
+}
+
+__global__ __launch_bounds__(256) void repeat_fill_kernel(const float* __restrict__ src, size_t n,
+                                                          float* __restrict__ dst, size_t total) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * 256) {
+    dst[i] = src[i % n];
+  }
+}
+
+__global__ __launch_bounds__(256) void postprocess_kernel(float* __restrict__ x, size_t n, float scale, float bias,
+                                                          int relu) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * 256) {
+    float v = x[i] * scale + bias;
+    if (relu && v < 0.0f) {
+      v = 0.0f;
+    }
+    x[i] = v;
+  }
+}
+
+}  // namespace lchip::k
+
+namespace lchip::kern {
+
+using namespace lchip::k;
+
+static int grid_for(size_t total) {
+  size_t blocks = (total + 255) / 256;
+  if (blocks > 65536) {
+    blocks = 65536;
+  }
+  return static_cast<int>(blocks < 1 ? 1 : blocks);
+}
+
+hipError_t convertPad(const float* src, uint16_t* dst, int batch, int rows, int cols, size_t ld_src, int rows_pad,
+                      int cols_pad, size_t src_bstride, size_t dst_bstride, Half t, hipStream_t stream) {
+  if (rows_pad <= 0 || cols_pad <= 0 || batch <= 0 || rows_pad > 65535) {
+    return hipErrorInvalidValue;
+  }
+  const dim3 grid((cols_pad + 1023) / 1024, rows_pad, batch);
+  if (t == Half::kBF16) {
+    hipLaunchKernelGGL((convert_pad_kernel<BF16>), grid, dim3(256), 0, stream, src, dst, rows, cols, ld_src, rows_pad,
+                       cols_pad, src_bstride, dst_bstride);
+  } else {
+    hipLaunchKernelGGL((convert_pad_kernel<F16>), grid, dim3(256), 0, stream, src, dst, rows, cols, ld_src, rows_pad,
+                       cols_pad, src_bstride, dst_bstride);
+  }
+  return hipGetLastError();
+}
+
+hipError_t convertTransposePad(const float* src, uint16_t* dst, int batch, int rows, int cols, size_t ld_src,
+                               int rows_pad, int cols_pad, size_t src_bstride, size_t dst_bstride, Half t,
+                               hipStream_t stream) {
+  if (rows_pad <= 0 || cols_pad <= 0 || batch <= 0) {
+    return hipErrorInvalidValue;
+  }
+  const dim3 grid((cols_pad + 63) / 64, (rows_pad + 31) / 32, batch);
+  if (t == Half::kBF16) {
+    hipLaunchKernelGGL((convert_transpose_pad_kernel<BF16>), grid, dim3(256), 0, stream, src, dst, rows, cols, ld_src,
+                       rows_pad, cols_pad, src_bstride, dst_bstride);
+  } else {
+    hipLaunchKernelGGL((convert_transpose_pad_kernel<F16>), grid, dim3(256), 0, stream, src, dst, rows, cols, ld_src,
+                       rows_pad, cols_pad, src_bstride, dst_bstride);
+  }
+  return hipGetLastError();
+}
+
+hipError_t im2colF32(const float* x, float* cols, int batch, int C, int H, int W, int kh, int kw, int sh, int sw,
+                     int ph, int pw, int oh, int ow, hipStream_t stream) {
+  const size_t total = static_cast<size_t>(batch) * oh * ow * C * kh * kw;
+  if (total == 0) {
+    return hipSuccess;
+  }
+  hipLaunchKernelGGL(im2col_f32_kernel, dim3(grid_for(total)), dim3(256), 0, stream, x, cols, C, H, W, kh, kw, sh, sw,
+                     ph, pw, oh, ow, total);
+  return hipGetLastError();
+}
+
+hipError_t repeatFillF32(const float* src, size_t n, float* dst, size_t total, hipStream_t stream) {
+  if (n == 0 || total == 0) {
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(repeat_fill_kernel, dim3(grid_for(total)), dim3(256), 0, stream, src, n, dst, total);
+  return hipGetLastError();
+}
+
+}  // namespace lchip::kern
+
+namespace lchip::kern {
+
+hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu, hipStream_t stream) {
+  if (n == 0) {
+    return hipSuccess;
+  }
+  hipLaunchKernelGGL(postprocess_kernel, dim3(grid_for(n)), dim3(256), 0, stream, x, n, scale, bias, relu);
+  return hipGetLastError();
+}
+
+}  // namespace lchip::kern

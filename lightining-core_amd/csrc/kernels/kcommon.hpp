@@ -1,0 +1,94 @@
+// kcommon.hpp -- types and device helpers shared by the gfx950 kernels.
+//
+// Lane layouts of the MFMA instructions used here (wave64, lane l):
+//   v_mfma_f32_32x32x2_f32   A: A[m = l%32][k = l/32]      B: B[k = l/32][n = l%32]
+//   v_mfma_f32_32x32x16_bf16 A: A[m = l%32][k = 8(l/32)+j] B: B[k = 8(l/32)+j][n = l%32], j = 0..7
+//   (f16 the same)
+//   32x32 accumulator (16 regs): D[m = 8(i/4) + 4(l/32) + i%4][n = l%32], i = 0..15
+// Any permutation of k applied identically to A and B leaves the product
+// unchanged; the attention kernels use that to feed softmax probabilities to
+// the second MFMA straight from the first MFMA's accumulator registers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lchip::k {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage tags for the two 16-bit MFMA input formats.
+struct BF16 {};
+struct F16 {};
+
+// fp32 -> bf16 bits, round to nearest even (NaN -> canonical quiet NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    return 0x7fc0u;
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// fp32 -> fp16 bits, round to nearest even (hardware conversion).
+__device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = static_cast<_Float16>(f);
+  return __builtin_bit_cast(uint16_t, h);
+}
+
+template <typename T>
+__device__ __forceinline__ uint16_t to_half_bits(float f);
+template <>
+__device__ __forceinline__ uint16_t to_half_bits<BF16>(float f) {
+  return f32_to_bf16_bits(f);
+}
+template <>
+__device__ __forceinline__ uint16_t to_half_bits<F16>(float f) {
+  return f32_to_f16_bits(f);
+}
+
+// Two fp32 values -> one packed dword of 16-bit values (lo in bits 0..15).
+template <typename T>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return static_cast<uint32_t>(to_half_bits<T>(lo)) | (static_cast<uint32_t>(to_half_bits<T>(hi)) << 16);
+}
+
+// 32x32x16 MFMA on 8 packed 16-bit values per lane (as four dwords).
+template <typename T>
+__device__ __forceinline__ floatx16 mfma32x32x16(u32x4 a, u32x4 b, floatx16 c);
+template <>
+__device__ __forceinline__ floatx16 mfma32x32x16<BF16>(u32x4 a, u32x4 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+template <>
+__device__ __forceinline__ floatx16 mfma32x32x16<F16>(u32x4 a, u32x4 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+
+__device__ __forceinline__ floatx16 mfma32x32x2f32(float a, float b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ floatx16 zero16() {
+  floatx16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    z[i] = 0.0f;
+  }
+  return z;
+}
+
+// Row (m) index held by accumulator register i of lane l in a 32x32 tile.
+__device__ __forceinline__ int acc_row(int i, int lane) {
+  return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+}
+
+}  // namespace lchip::k

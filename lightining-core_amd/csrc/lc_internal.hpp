@@ -1,0 +1,119 @@
+// lc_internal.hpp -- internal types of the HIP backend library.
+//
+// Mirrors the reference's runtime vocabulary (include/lightning_core/core/
+// runtime.hpp:11-83): Device, Status, trace events and op kinds, with
+// Device::kHIP appended as value 3 so the 4-bit dispatch-trace encoding
+// (src/runtime.cpp:703-708) carries it unchanged.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <mutex>
+#include <string>
+
+#include "lightning_core_hip.h"
+
+namespace lchip {
+
+enum class Status { kSuccess = 0, kNotInitialized, kInvalidValue, kOutOfMemory, kNotSupported, kDriverError, kUnknown };
+enum class Device { kCPU = 0, kCUDA = 1, kMetal = 2, kHIP = 3 };
+
+enum class TraceEventType {
+  kMallocDevice = 0,
+  kFreeDevice,
+  kMemcpy,
+  kDeviceSynchronize,
+  kApplySyncPolicy,
+  kGetDeviceCount,
+  kIsCudaAvailable,
+  kIsMetalAvailable,
+  kPreferredDeviceFor,
+  kBackendName,
+  kOpDispatch
+};
+
+enum class TraceOp { kUnknown = 0, kMatMul, kVectorAdd, kMatrixSub, kMatrixDiv, kConv2dNchw, kAttentionForward };
+
+inline lcError_t toLc(Status s) { return static_cast<lcError_t>(static_cast<int>(s)); }
+inline Device fromLc(lcDeviceKind d) { return static_cast<Device>(static_cast<int>(d)); }
+inline bool validDevice(lcDeviceKind d) { return d >= LC_DEVICE_CPU && d <= LC_DEVICE_HIP; }
+
+// Thread-local last error message (lcGetLastErrorMessage).
+void setLastError(const std::string& msg);
+const char* lastError();
+Status fail(Status st, const std::string& msg);
+Status failHip(hipError_t e, const char* what);
+
+#define LC_HIP_TRY(expr)                          \
+  do {                                            \
+    hipError_t lc_e_ = (expr);                    \
+    if (lc_e_ != hipSuccess) {                    \
+      return ::lchip::failHip(lc_e_, #expr);      \
+    }                                             \
+  } while (0)
+
+#define LC_TRY(expr)                              \
+  do {                                            \
+    ::lchip::Status lc_s_ = (expr);               \
+    if (lc_s_ != ::lchip::Status::kSuccess) {     \
+      return lc_s_;                               \
+    }                                             \
+  } while (0)
+
+// ---- runtime trace (ring of 4096 events, off by default) --------------------
+constexpr std::size_t kTraceCapacity = 4096;
+void traceRecord(TraceEventType type, Status st, std::size_t size_bytes = 0, int d0 = 0, int d1 = 0);
+void traceOpDispatch(TraceOp op, Device requested, Device selected, bool fallback, std::size_t workload_hint);
+int encodeDispatch(Device requested, Device selected, bool fallback);
+
+// ---- HIP device context --------------------------------------------------------
+// One context per process for the single visible gfx950 device: one
+// non-blocking stream (default priority) that every kernel, copy and event of
+// the library uses, and one mutex that serialises host-side use of shared
+// buffers (the reference serialises its attention backend the same way,
+// src/attention_metal.mm:1855).
+struct HipContext {
+  std::recursive_mutex mu;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipDeviceProp_t props{};
+};
+
+bool hipAvailable();
+// Returns the context, or nullptr with the status set (kNotSupported when no
+// gfx950 device is visible).
+HipContext* hipContext(Status* st);
+
+// Device allocation that grows (1.5x, like the reference's Metal buffers,
+// src/attention_metal.mm:150-164) and never shrinks.  Contents are not kept
+// across growth.  Freed by reset() or the destructor.
+class DeviceBuffer {
+ public:
+  DeviceBuffer() = default;
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  ~DeviceBuffer() { reset(); }
+  Status ensure(std::size_t bytes, bool zero = false);
+  void reset();
+  void* get() const { return ptr_; }
+  template <typename T>
+  T* as() const {
+    return static_cast<T*>(ptr_);
+  }
+  std::size_t size() const { return bytes_; }
+
+ private:
+  void* ptr_ = nullptr;
+  std::size_t bytes_ = 0;
+};
+
+// Upload / download on the context stream (pageable host memory).
+Status upload(HipContext* ctx, void* dst, const void* src, std::size_t bytes);
+Status download(HipContext* ctx, void* dst, const void* src, std::size_t bytes);
+Status syncStream(HipContext* ctx);
+
+inline std::size_t roundUp(std::size_t v, std::size_t m) { return (v + m - 1) / m * m; }
+
+}  // namespace lchip

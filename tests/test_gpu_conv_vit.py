@@ -1,0 +1,91 @@
+"""conv2d, the conv -> attention pipeline and the ViT block on the hip device.
+
+conv2d vs the oracle's im2col path (core/ops.hpp:855-1213) on the golden
+vectors and extra geometries; conv_attention_torchstrong_nchw vs the golden
+vectors of bind_integrated.cpp:614-730 (flat slices and QkvPackRepeat);
+the ViT block (fp16) vs the oracle composition on the
+rows of two whole images (every stage of those images is exercised).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib
+from gpu_util import assert_parity, note, require_hip
+from lightning_core import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lc():
+    return require_hip()
+
+
+@pytest.mark.parametrize("case", oracle_lib.golden_cases("conv_"), ids=lambda c: c["name"])
+def test_conv_golden(lc, case):
+    p = case["params"]
+    x = oracle_lib.golden_input(case, "x").reshape(p["batch"], p["in_c"], p["in_h"], p["in_w"])
+    w = oracle_lib.golden_input(case, "w").reshape(p["out_c"], p["in_c"], p["kh"], p["kw"])
+    bias = oracle_lib.golden_input(case, "bias")
+    exp = np.asarray(case["expected"], np.float32)
+    if p["op"] == "conv2d_nchw":
+        got = lc.conv2d_nchw(x, w, bias, p["stride_h"], p["stride_w"], p["pad_h"], p["pad_w"],
+                             apply_relu=p["relu"]).ravel()
+        assert oracle_lib.elementwise_ok(exp, got, 1.5e-2, 1.5e-2)
+    else:
+        got = lc.api.conv_attention_torchstrong_nchw(x, w, bias, p["seq_len"], p["head_dim"], p["stride_h"],
+                                                     p["stride_w"], p["pad_h"], p["pad_w"])
+    assert_parity(exp, got, "f32", case["name"])
+
+
+@pytest.mark.parametrize("xs,ws,stride,pad", [((2, 3, 17, 19), (5, 3, 3, 3), (1, 1), (1, 1)),
+                                              ((1, 4, 16, 16), (8, 4, 1, 1), (1, 1), (0, 0)),
+                                              ((2, 3, 64, 64), (16, 3, 16, 16), (16, 16), (0, 0))])
+def test_conv_extra(lc, oracle, xs, ws, stride, pad):
+    x, w = synth.normal(xs, stream=1), synth.normal(ws, stream=2)
+    bias = synth.normal((ws[0],), stream=3)
+    for relu in (False, True):
+        got = lc.conv2d_nchw(x, w, bias, stride[0], stride[1], pad[0], pad[1], apply_relu=relu)
+        assert_parity(oracle.conv2d(x, w, bias, stride, pad, relu), got, "f32", f"conv {xs} {ws} relu={relu}")
+
+
+def test_conv_attention_graph_mode_matches_eager(lc):
+    x, w = synth.normal((1, 3, 8, 8), stream=4), synth.normal((8, 3, 3, 3), stream=5)
+    e = lc.api.conv_attention_torchstrong_nchw(x, w, None, 16, 16, 1, 1, 1, 1, execution_mode="eager")
+    g = lc.api.conv_attention_torchstrong_nchw(x, w, None, 16, 16, 1, 1, 1, 1, execution_mode="graph")
+    np.testing.assert_array_equal(e, g)
+
+
+def _vit_inputs(bn, c, img, p, e):
+    x = synth.uniform((bn, c, img, img), lo=0.0, hi=1.0, stream=30)
+    w_conv = synth.normal((e, c, p, p), std=0.02, stream=31)
+    w_qkv = synth.normal((e, 3 * e), std=0.02, stream=32)
+    w_o = synth.normal((e, e), std=0.02, stream=33)
+    return x, w_conv, w_qkv, w_o
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_vit_block_small(lc, oracle, dtype):
+    bn, c, img, p, e, heads = 2, 3, 64, 16, 128, 2
+    x, w_conv, w_qkv, w_o = _vit_inputs(bn, c, img, p, e)
+    got = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype=dtype)
+    ref = oracle.vit_block(*(synth.round_to(t, dtype) for t in (x, w_conv, w_qkv, w_o)), heads)
+    assert_parity(ref, got.reshape(ref.shape), dtype, f"vit small {dtype}")
+
+
+def test_vit_block_config4(lc, oracle):
+    bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12
+    note("[case] config 4 ViT block")
+    x, w_conv, w_qkv, w_o = _vit_inputs(bn, c, img, p, e)
+    s = lc.VitBlockSession(bn, c, img, img, p, e, heads, "f16")
+    s.set_weights(w_conv, w_qkv, w_o)
+    got = s.forward(x)
+    s.run_cached(3)
+    again = s.forward(None)
+    np.testing.assert_array_equal(got, again)  # deterministic, resident input
+    t = s.tokens
+    xr, wcr, wqr, wor = (synth.round_f16(a) for a in (x, w_conv, w_qkv, w_o))
+    for img_idx in (0, bn - 1):
+        rows = (img_idx * t, (img_idx + 1) * t)
+        ref = oracle.vit_block(xr, wcr, wqr, wor, heads, rows=rows)
+        assert_parity(ref, got.reshape(bn * t, e)[rows[0]:rows[1]], "f16", f"config4 image {img_idx}")

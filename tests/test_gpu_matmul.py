@@ -1,0 +1,146 @@
+"""matmul2d on the hip device vs the CPU oracle (src/ops/matmul_cpu.cpp:49-60).
+
+Covers the reference's own cases (tests/test_matmul.cpp known answer,
+tests/test_backend_parity.cpp 4x7x5 with atol 2e-3 / rtol 3e-3), the golden
+vectors, BASELINE config 2 (fp32 1024^3 and 1000x1030x777) in full, config 5
+(bf16 4096^3, 8192^3 on sampled rows plus a full-tensor column-checksum, and
+the skinny 16x8192x8192 in full), the resident-session protocol and the
+policy-level null-pointer contract.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib
+from gpu_util import assert_parity, note, require_hip
+from lightning_core import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lc():
+    return require_hip()
+
+
+def test_matmul_kat(lc):
+    a = np.arange(1, 7, dtype=np.float32).reshape(2, 3)
+    b = np.arange(7, 13, dtype=np.float32).reshape(3, 2)
+    out = lc.matmul2d(a, b)
+    np.testing.assert_allclose(out, [[58, 64], [139, 154]], atol=1e-4)
+
+
+@pytest.mark.parametrize("case", oracle_lib.golden_cases("matmul"), ids=lambda c: c["name"])
+def test_matmul_golden(lc, case):
+    p = case["params"]
+    a = oracle_lib.golden_input(case, "a").reshape(p["m"], p["k"])
+    b = oracle_lib.golden_input(case, "b").reshape(p["k"], p["n"])
+    got = lc.matmul2d(a, b)
+    exp = np.asarray(case["expected"], np.float32).reshape(p["m"], p["n"])
+    assert_parity(exp, got, "f32", case["name"])
+    assert oracle_lib.elementwise_ok(exp, got, 2e-3, 3e-3)
+
+
+@pytest.mark.parametrize("m,k,n", [(1024, 1024, 1024), (1000, 777, 1030), (64, 64, 64), (1, 5, 300), (333, 17, 65)])
+def test_matmul_f32_config2(lc, oracle, m, k, n):
+    a = synth.uniform((m, k), stream=1)
+    b = synth.uniform((k, n), stream=2)
+    got = lc.matmul2d(a, b)
+    assert_parity(oracle.matmul(a, b), got, "f32", f"f32 {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("m,k,n", [(256, 320, 200), (300, 64, 520), (16, 512, 96), (7, 64, 1000), (1, 128, 33)])
+def test_matmul_half_small(lc, oracle, dtype, m, k, n):
+    a = synth.normal((m, k), stream=3)
+    b = synth.normal((k, n), stream=4)
+    s = lc.MatMulResidentSession(m, k, n, dtype)
+    s.start_into(a, b)
+    got = s.finish_into().reshape(m, n)
+    ref = oracle.matmul(synth.round_to(a, dtype), synth.round_to(b, dtype))
+    assert_parity(ref, got, dtype, f"{dtype} {m}x{k}x{n}")
+
+
+def _colsum_check(a_r, b_r, got):
+    # checksum of checksums: column sums of C equal (column sums of A) . B
+    ref = np.asarray(a_r, np.float64).sum(axis=0) @ np.asarray(b_r, np.float64)
+    err = oracle_lib.normwise_rel(ref, np.asarray(got, np.float64).sum(axis=0))
+    note(f"[parity] colsum normwise_rel={err:.3e}")
+    assert err <= 2e-3
+
+
+@pytest.mark.parametrize("size", [4096, 8192])
+def test_matmul_bf16_config5_sampled(lc, oracle, size):
+    m = k = n = size
+    note(f"[case] bf16 GEMM {size}^3 generating inputs")
+    a = synth.normal((m, k), stream=5)
+    b = synth.normal((k, n), stream=6)
+    s = lc.MatMulResidentSession(m, k, n, "bf16")
+    s.start_into(a, b)
+    s.run_batch_sync_cached_no_download(3)
+    got = s.finish_into().reshape(m, n)
+    a_r, b_r = synth.round_bf16(a), synth.round_bf16(b)
+    rows = np.unique(np.concatenate([np.arange(0, 32), np.linspace(32, m - 33, 16).astype(int), np.arange(m - 16, m)]))
+    note(f"[case] oracle on {rows.size} sampled rows")
+    for r0 in range(0, rows.size, 8):
+        rr = rows[r0:r0 + 8]
+        ref = np.concatenate([oracle.matmul(a_r, b_r, rows=(int(r), int(r) + 1)) for r in rr])
+        assert_parity(ref, got[rr], "bf16", f"bf16 {size}^3 rows {rr[0]}..{rr[-1]}")
+    _colsum_check(a_r, b_r, got)
+
+
+def test_matmul_bf16_skinny_config5(lc, oracle):
+    m, k, n = 16, 8192, 8192
+    a = synth.normal((m, k), stream=7)
+    b = synth.normal((k, n), stream=8)
+    s = lc.MatMulResidentSession(m, k, n, "bf16")
+    s.start_into(a, b)
+    got = s.finish_into().reshape(m, n)
+    ref = oracle.matmul(synth.round_bf16(a), synth.round_bf16(b))
+    assert_parity(ref, got, "bf16", "bf16 skinny 16x8192x8192")
+
+
+def test_resident_session_protocol(lc, oracle):
+    m, k, n = 96, 80, 72
+    a = synth.uniform((m, k), stream=9)
+    b = synth.uniform((k, n), stream=10)
+    s = lc.MatMulResidentSession(m, k, n, "f32")
+    out = s.start_into(a, b)  # no download: out untouched
+    assert not out.any()
+    s.run_into()
+    s.sync_into()
+    s.run_batch_sync_into(a, b, np.zeros(m * n, np.float32), 5)
+    s.run_batch_sync_cached_no_download(4)
+    got = s.finish_into().reshape(m, n)
+    assert_parity(oracle.matmul(a, b), got, "f32", "resident protocol")
+    # a second session of another shape does not disturb the first
+    s2 = lc.MatMulResidentSession(8, 8, 8, "f32")
+    s2.start_into(np.eye(8), np.eye(8))
+    np.testing.assert_allclose(s2.finish_into().reshape(8, 8), np.eye(8))
+    assert_parity(oracle.matmul(a, b), s.finish_into().reshape(m, n), "f32", "resident after other session")
+
+
+def test_policy_null_pointers_use_resident(lc, oracle):
+    m, k, n = 40, 30, 20
+    a = synth.uniform((m, k), stream=11)
+    b = synth.uniform((k, n), stream=12)
+    start = lc.MatMulIoPolicy(upload_a=True, upload_b=True, download_out=False, synchronize=False)
+    lc.matmul_with_policy(a, b, m, k, n, policy=start)
+    run = lc.MatMulIoPolicy(upload_a=False, upload_b=False, download_out=True, synchronize=True)
+    got = lc.matmul_with_policy(None, None, m, k, n, policy=run).reshape(m, n)
+    assert_parity(oracle.matmul(a, b), got, "f32", "policy resident")
+    # a null pointer that the policy needs is an invalid value (ops.hpp:367-370)
+    with pytest.raises(RuntimeError, match="invalid value"):
+        lc.matmul_with_policy(None, b, m, k, n, policy=lc.MatMulIoPolicy())
+
+
+def test_trace_records_hip_dispatch(lc):
+    lc.runtime_trace_clear()
+    lc.runtime_trace_enable(True)
+    try:
+        lc.matmul2d(np.ones((4, 7), np.float32), np.ones((7, 5), np.float32))
+    finally:
+        lc.runtime_trace_enable(False)
+    ev = [e for e in lc.runtime_trace_events() if e["type"] == "op_dispatch"]
+    assert ev and ev[-1]["op"] == "matmul"
+    assert ev[-1]["requested"] == "hip" and ev[-1]["selected"] == "hip" and not ev[-1]["fallback"]
+    assert ev[-1]["size_bytes"] == 4 * 7 * 5
