@@ -63,7 +63,6 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restric
   float m_run = kMaskValue;
   float l_run = 0.0f;
   const int qi = q0 + (lane & 31);
-  const float c = scale * kLog2e;
   const int kend = causal ? min(S, q0 + 32) : S;
 
   for (int j0 = 0; j0 < kend; j0 += 32) {
@@ -124,7 +123,6 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restric
         o[t] = mfma32x32x2f32(a, st[s], o[t]);
       }
     }
-    (void)c;
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
@@ -151,9 +149,13 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restric
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit: 4 waves x 32 queries per workgroup, 64-key tiles, K tile and V^T
-// tile in LDS, Q fragments in registers, v_mfma_f32_32x32x16_{bf16,f16}.
+// 16-bit: 4 waves x 32 queries per workgroup, 64-key tiles.  K tile and V^T
+// tile are double-buffered in LDS; the next tile is prefetched into registers
+// while the current one is computed, so each tile costs one barrier.  Q
+// fragments live in registers; v_mfma_f32_32x32x16_{bf16,f16}.
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* __restrict__ Q,
                                                                const uint16_t* __restrict__ K,
@@ -165,8 +167,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   constexpr int LDV = KT + 8;
   constexpr int DT = D / 32;
   constexpr int QS = D / 16;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[KT * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[D * LDV];
+  constexpr int KCH = KT * D / 8 / 256;  // 16-byte chunks of the K tile per thread
+  constexpr int VCH = D * KT / 8 / 256;  // ... of the V^T tile
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][D * LDV];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -181,6 +185,41 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   const uint16_t* Vh = Vt + hoff;
   const int lrow = lane & 31;
   const int half = lane >> 5;
+
+  u32x4 kreg[KCH];
+  u32x4 vreg[VCH];
+  auto load_tile = [&](int j0) {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int ch = c * 256 + tid;
+      const int r = ch / (D / 8);
+      const int col = (ch - r * (D / 8)) * 8;
+      kreg[c] = *reinterpret_cast<const u32x4*>(Kh + static_cast<size_t>(j0 + r) * D + col);
+    }
+#pragma unroll
+    for (int c = 0; c < VCH; ++c) {
+      const int ch = c * 256 + tid;
+      const int r = ch / (KT / 8);
+      const int col = (ch - r * (KT / 8)) * 8;
+      vreg[c] = *reinterpret_cast<const u32x4*>(Vh + static_cast<size_t>(r) * S_pad + j0 + col);
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int c = 0; c < KCH; ++c) {
+      const int ch = c * 256 + tid;
+      const int r = ch / (D / 8);
+      const int col = (ch - r * (D / 8)) * 8;
+      *reinterpret_cast<u32x4*>(&Ks[buf][r * LDK + col]) = kreg[c];
+    }
+#pragma unroll
+    for (int c = 0; c < VCH; ++c) {
+      const int ch = c * 256 + tid;
+      const int r = ch / (KT / 8);
+      const int col = (ch - r * (KT / 8)) * 8;
+      *reinterpret_cast<u32x4*>(&Vs[buf][r * LDV + col]) = vreg[c];
+    }
+  };
 
   u32x4 qf[QS];
 #pragma unroll
@@ -198,94 +237,93 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   const float c = scale * kLog2e;
   const int kend = causal ? min(S, qb * 128 + 128) : S;
 
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  int buf = 0;
   for (int j0 = 0; j0 < kend; j0 += KT) {
-    __syncthreads();
-    for (int ch = tid; ch < KT * D / 8; ch += 256) {
-      const int r = ch / (D / 8);
-      const int col = (ch - r * (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&Ks[r * LDK + col]) =
-          *reinterpret_cast<const u32x4*>(Kh + static_cast<size_t>(j0 + r) * D + col);
+    const bool more = j0 + KT < kend;
+    if (more) {
+      load_tile(j0 + KT);
     }
-    for (int ch = tid; ch < D * KT / 8; ch += 256) {
-      const int r = ch / (KT / 8);
-      const int col = (ch - r * (KT / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&Vs[r * LDV + col]) =
-          *reinterpret_cast<const u32x4*>(Vh + static_cast<size_t>(r) * S_pad + j0 + col);
-    }
-    __syncthreads();
-    if (causal && j0 > q0 + 31) {
-      continue;  // every key of this tile is after every query of this wave
-    }
-
-    floatx16 sc[2];
+    if (!(causal && j0 > q0 + 31)) {  // else every key of the tile follows every query of this wave
+      const uint16_t* ks = Ks[buf];
+      const uint16_t* vs = Vs[buf];
+      floatx16 sc[2];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      sc[kt] = zero16();
+      for (int kt = 0; kt < 2; ++kt) {
+        sc[kt] = zero16();
 #pragma unroll
-      for (int s = 0; s < QS; ++s) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(&Ks[(kt * 32 + lrow) * LDK + s * 16 + 8 * half]);
-        sc[kt] = mfma32x32x16<T>(a, qf[s], sc[kt]);
-      }
-    }
-    const bool need_mask = (j0 + KT > S) || (causal && j0 + KT - 1 > q0);
-    float mt = kMaskValue;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float x = sc[kt][i] * c;
-        if (need_mask) {
-          const int key = j0 + kt * 32 + acc_row(i, lane);
-          if (key >= S || (causal && key > qi)) {
-            x = kMaskValue;
-          }
+        for (int s = 0; s < QS; ++s) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(&ks[(kt * 32 + lrow) * LDK + s * 16 + 8 * half]);
+          sc[kt] = mfma32x32x16<T>(a, qf[s], sc[kt]);
         }
-        sc[kt][i] = x;
-        mt = fmaxf(mt, x);
       }
-    }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = exp2f(m_run - m_new);
-    float ls = 0.0f;
+      const bool need_mask = (j0 + KT > S) || (causal && j0 + KT - 1 > q0);
+      float mt = kMaskValue;
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
+      for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = exp2f(sc[kt][i] - m_new);
-        sc[kt][i] = p;
-        ls += p;
+        for (int i = 0; i < 16; ++i) {
+          float x = sc[kt][i] * c;
+          if (need_mask) {
+            const int key = j0 + kt * 32 + acc_row(i, lane);
+            if (key >= S || (causal && key > qi)) {
+              x = kMaskValue;
+            }
+          }
+          sc[kt][i] = x;
+          mt = fmaxf(mt, x);
+        }
       }
-    }
-    l_run = l_run * alpha + ls;
-    m_run = m_new;
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = fast_exp2(m_run - m_new);
+      float ls = 0.0f;
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
+      for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        o[t][i] *= alpha;
+        for (int i = 0; i < 16; ++i) {
+          const float p = fast_exp2(sc[kt][i] - m_new);
+          sc[kt][i] = p;
+          ls += p;
+        }
       }
-    }
-    // O^T += V^T . P^T over 4 key-steps of 16; element j of step ks is key
-    // 16*ks + 8*(j/4) + 4*half + j%4 = accumulator register 8*(ks&1) + j of sc[ks>>1].
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const floatx16& p = sc[ks >> 1];
-      const int b0 = (ks & 1) * 8;
-      u32x4 pb;
-      pb[0] = pack2<T>(p[b0 + 0], p[b0 + 1]);
-      pb[1] = pack2<T>(p[b0 + 2], p[b0 + 3]);
-      pb[2] = pack2<T>(p[b0 + 4], p[b0 + 5]);
-      pb[3] = pack2<T>(p[b0 + 6], p[b0 + 7]);
+      l_run = l_run * alpha + ls;
+      m_run = m_new;
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
-        const uint16_t* vp = &Vs[(t * 32 + lrow) * LDV + 16 * ks + 4 * half];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vp);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vp + 8);
-        const u32x4 va{lo[0], lo[1], hi[0], hi[1]};
-        o[t] = mfma32x32x16<T>(va, pb, o[t]);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          o[t][i] *= alpha;
+        }
+      }
+      // O^T += V^T . P^T over 4 key-steps of 16; element j of step ks is key
+      // 16*ks + 8*(j/4) + 4*half + j%4 = accumulator register 8*(ks&1) + j of sc[ks>>1].
+#pragma unroll
+      for (int ks2 = 0; ks2 < 4; ++ks2) {
+        const floatx16& p = sc[ks2 >> 1];
+        const int b0 = (ks2 & 1) * 8;
+        u32x4 pb;
+        pb[0] = pack2<T>(p[b0 + 0], p[b0 + 1]);
+        pb[1] = pack2<T>(p[b0 + 2], p[b0 + 3]);
+        pb[2] = pack2<T>(p[b0 + 4], p[b0 + 5]);
+        pb[3] = pack2<T>(p[b0 + 6], p[b0 + 7]);
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+          const uint16_t* vp = &vs[(t * 32 + lrow) * LDV + 16 * ks2 + 4 * half];
+          const u32x2 lo = *reinterpret_cast<const u32x2*>(vp);
+          const u32x2 hi = *reinterpret_cast<const u32x2*>(vp + 8);
+          const u32x4 va{lo[0], lo[1], hi[0], hi[1]};
+          o[t] = mfma32x32x16<T>(va, pb, o[t]);
+        }
       }
     }
+    if (more) {
+      store_tile(buf ^ 1);
+    }
+    __syncthreads();
+    buf ^= 1;
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);

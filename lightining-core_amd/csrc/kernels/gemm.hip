@@ -302,10 +302,18 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_kernel(LoadA load_a,
   const int wm = (wave / WN) * (BM / WM);
   const int wn = (wave % WN) * (BN / WN);
 
-  // Grouped tile order: 8 tile-rows share their B column panels in L2.
+  // Block -> tile mapping.  The dispatcher hands workgroup i to XCD i % 8;
+  // remap so each XCD receives a contiguous run of the grouped tile order
+  // (tiles that share A row panels and B column panels), which then hit in
+  // that XCD's own L2.  Grouped order: 8 tile-rows share their B panels.
   constexpr int GROUP = 8;
   const int tiles_m = (M + BM - 1) / BM;
-  const int pid = blockIdx.x;
+  const int nwg = gridDim.x;
+  const int full = nwg & ~7;
+  int pid = blockIdx.x;
+  if (pid < full) {
+    pid = (pid & 7) * (full >> 3) + (pid >> 3);
+  }
   const int group_size = GROUP * tiles_n;
   const int group = pid / group_size;
   const int first_m = group * GROUP;
@@ -514,18 +522,50 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
   }
 }
 
-constexpr int kHBM = 128;
-constexpr int kHBN = 128;
 constexpr int kHBK = 64;
+
+// Tile configurations (block tile BM x BN, waves WM x WN):
+//   big   256x256, 8 waves (2 x 4, 128x64 each), 147 KB LDS double buffer
+//   mid   128x128, 4 waves (2 x 2, 64x64 each)
+//   small  64x64,  4 waves (2 x 2, 32x32 each)
+// The largest tile that still gives at least one workgroup per CU is used.
+enum class HalfTile { kBig, kMid, kSmall };
+
+inline int tiles_for(int M, int N, int b) { return ((M + b - 1) / b) * ((N + b - 1) / b); }
+
+inline HalfTile pick_half_tile(int M, int N) {
+  constexpr int kCUs = 256;
+  if (tiles_for(M, N, 256) >= kCUs) {
+    return HalfTile::kBig;
+  }
+  if (tiles_for(M, N, 128) >= kCUs) {
+    return HalfTile::kMid;
+  }
+  return HalfTile::kSmall;
+}
+
+template <typename T, int BM, int BN, int WM, int WN, typename LoadA, typename Epi>
+static hipError_t launch_gemm_half_cfg(LoadA load_a, const uint16_t* Bt, int M, int N, int K, int ldb, Epi epi,
+                                       hipStream_t stream) {
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles_n = (N + BN - 1) / BN;
+  hipLaunchKernelGGL((gemm_half_tn_kernel<T, BM, BN, kHBK, WM, WN, LoadA, Epi>), dim3(tiles_m * tiles_n),
+                     dim3(WM * WN * 64), 0, stream, load_a, Bt, M, N, K, ldb, tiles_n, epi);
+  return hipGetLastError();
+}
 
 template <typename T, typename LoadA, typename Epi>
 static hipError_t launch_gemm_half(LoadA load_a, const uint16_t* Bt, int M, int N, int K, int ldb, Epi epi,
                                    hipStream_t stream) {
-  const int tiles_m = (M + kHBM - 1) / kHBM;
-  const int tiles_n = (N + kHBN - 1) / kHBN;
-  hipLaunchKernelGGL((gemm_half_tn_kernel<T, kHBM, kHBN, kHBK, 2, 2, LoadA, Epi>), dim3(tiles_m * tiles_n), dim3(256),
-                     0, stream, load_a, Bt, M, N, K, ldb, tiles_n, epi);
-  return hipGetLastError();
+  switch (pick_half_tile(M, N)) {
+    case HalfTile::kBig:
+      return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
+    case HalfTile::kMid:
+      return launch_gemm_half_cfg<T, 128, 128, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
+    case HalfTile::kSmall:
+    default:
+      return launch_gemm_half_cfg<T, 64, 64, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
+  }
 }
 
 }  // namespace lchip::k
