@@ -259,45 +259,58 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
           sc[kt] = mfma32x32x16<T>(a, qf[s], sc[kt]);
         }
       }
+      // Raw scores s = q.k; the scale is applied inside the exponent:
+      // p = exp2(s*c - m*c) with m the running max of raw scores (c > 0).
       const bool need_mask = (j0 + KT > S) || (causal && j0 + KT - 1 > q0);
+      if (need_mask) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = j0 + kt * 32 + acc_row(i, lane);
+            if (key >= S || (causal && key > qi)) {
+              sc[kt][i] = kMaskValue;
+            }
+          }
+        }
+      }
       float mt = kMaskValue;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          float x = sc[kt][i] * c;
-          if (need_mask) {
-            const int key = j0 + kt * 32 + acc_row(i, lane);
-            if (key >= S || (causal && key > qi)) {
-              x = kMaskValue;
-            }
-          }
-          sc[kt][i] = x;
-          mt = fmaxf(mt, x);
+          mt = fmaxf(mt, sc[kt][i]);
         }
       }
       mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = fast_exp2(m_run - m_new);
+      // Rescale O and l only when some lane's max grew by more than 8/c
+      // (exp2 units); otherwise keep the stale reference max.  O and l always
+      // share the same reference, so O/l is unchanged; exponents stay <= 8.
+      const float m_cand = fmaxf(m_run, mt);
+      if (__any((m_cand - m_run) * c > 8.0f)) {
+        const float alpha = fast_exp2((m_run - m_cand) * c);
+        m_run = m_cand;
+        l_run *= alpha;
+#pragma unroll
+        for (int t = 0; t < DT; ++t) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            o[t][i] *= alpha;
+          }
+        }
+      }
+      const float mc = m_run * c;
       float ls = 0.0f;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float p = fast_exp2(sc[kt][i] - m_new);
+          const float p = fast_exp2(__builtin_fmaf(sc[kt][i], c, -mc));
           sc[kt][i] = p;
           ls += p;
         }
       }
-      l_run = l_run * alpha + ls;
-      m_run = m_new;
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          o[t][i] *= alpha;
-        }
-      }
+      l_run += ls;
       // O^T += V^T . P^T over 4 key-steps of 16; element j of step ks is key
       // 16*ks + 8*(j/4) + 4*half + j%4 = accumulator register 8*(ks&1) + j of sc[ks>>1].
 #pragma unroll

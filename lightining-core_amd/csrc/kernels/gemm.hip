@@ -12,6 +12,10 @@
 //    The A-tile loader and the epilogue are policies, so the same main loop
 //    serves the plain GEMM, the implicit-GEMM patch-embed convolution and the
 //    QKV projection that writes head-major Q/K and transposed V.
+#include <stdlib.h>
+
+#include <string>
+
 #include "../kernels.hpp"
 #include "kcommon.hpp"
 
@@ -280,7 +284,7 @@ struct EpiQKV {
   }
 };
 
-template <typename T, int BM, int BN, int BK, int WM, int WN, typename LoadA, typename Epi>
+template <typename T, int BM, int BN, int BK, int WM, int WN, int STORE_AT, typename LoadA, typename Epi>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_kernel(LoadA load_a, const uint16_t* __restrict__ Bt,
                                                                     int M, int N, int K, int ldb, int tiles_n,
                                                                     Epi epi) {
@@ -381,6 +385,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_kernel(LoadA load_a,
     }
 #pragma unroll
     for (int kk = 0; kk < BK; kk += 16) {
+      // The next stage goes to the other LDS buffer half-way through this
+      // stage's MFMAs, so the store (and its wait on the global loads)
+      // overlaps matrix work instead of following it.
+      if (kk == STORE_AT && more) {
+        store(buf ^ 1);
+      }
       u32x4 af[TM];
       u32x4 bf[TN];
 #pragma unroll
@@ -399,7 +409,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_kernel(LoadA load_a,
         }
       }
     }
-    if (more) {
+    if (STORE_AT >= BK && more) {
       store(buf ^ 1);
     }
     __syncthreads();
@@ -444,11 +454,12 @@ __device__ __forceinline__ floatx4 mfma16x16x32<F16>(u32x4 a, u32x4 b, floatx4 c
                                                 0);
 }
 
-template <typename T, int NT>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __restrict__ A,
-                                                          const uint16_t* __restrict__ Bt, float* __restrict__ C,
-                                                          int M, int N, int K, int lda, int ldb, int ldc) {
-  __shared__ floatx4 red[4][NT][64];
+template <typename T, int NT, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(const uint16_t* __restrict__ A,
+                                                                  const uint16_t* __restrict__ Bt,
+                                                                  float* __restrict__ C, int M, int N, int K,
+                                                                  int lda, int ldb, int ldc) {
+  __shared__ floatx4 red[WAVES][NT][64];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int n0 = blockIdx.x * 16 * NT;
@@ -465,17 +476,18 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
   for (int t = 0; t < NT; ++t) {
     acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   }
+  // Waves take interleaved 32-wide k-steps: wave w handles w, w+WAVES, ...
   const int steps = K / 32;
   int s = wave;
-  for (; s + 12 < steps; s += 16) {
+  for (; s + 3 * WAVES < steps; s += 4 * WAVES) {
     u32x4 a[4];
     u32x4 b[4][NT];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      a[u] = *reinterpret_cast<const u32x4*>(arow + (s + 4 * u) * 32);
+      a[u] = *reinterpret_cast<const u32x4*>(arow + (s + WAVES * u) * 32);
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
-        b[u][t] = *reinterpret_cast<const u32x4*>(brow[t] + (s + 4 * u) * 32);
+        b[u][t] = *reinterpret_cast<const u32x4*>(brow[t] + (s + WAVES * u) * 32);
       }
     }
 #pragma unroll
@@ -486,7 +498,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
       }
     }
   }
-  for (; s < steps; s += 4) {
+  for (; s < steps; s += WAVES) {
     const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
@@ -502,7 +514,7 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
     const int t = wave;
     floatx4 v = red[0][t][lane];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) {
+    for (int w = 1; w < WAVES; ++w) {
       const floatx4 o = red[w][t][lane];
       v[0] += o[0];
       v[1] += o[1];
@@ -524,19 +536,214 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(const uint16_t* __rest
 
 constexpr int kHBK = 64;
 
-// Tile configurations (block tile BM x BN, waves WM x WN):
-//   big   256x256, 8 waves (2 x 4, 128x64 each), 147 KB LDS double buffer
-//   mid   128x128, 4 waves (2 x 2, 64x64 each)
-//   small  64x64,  4 waves (2 x 2, 32x32 each)
-// The largest tile that still gives at least one workgroup per CU is used.
-enum class HalfTile { kBig, kMid, kSmall };
+// 16-byte global -> LDS copy of one lane (LDS address = lds_base + 16*lane).
+// A plain (non-template) device function: used directly inside a kernel
+// template whose body depends on template parameters, the target builtin
+// makes the host-side instantiation fail silently and no launch stub is
+// emitted.
+__device__ __forceinline__ void load_lds16(const uint16_t* src, uint16_t* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+}
+
+// Workgroup barrier without the release fence of __syncthreads(): the fence
+// would make the compiler drain every outstanding global -> LDS load
+// (vmcnt(0)) at each stage and collapse a multi-stage pipeline.  Callers wait
+// for exactly the stage they need with s_waitcnt vmcnt(n) first; every LDS
+// read of the retiring stage has already been consumed by its MFMA.  The empty
+// asm statements keep the compiler from moving memory operations across.
+__device__ __forceinline__ void stage_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// ---------------------------------------------------------------------------
+// Large-tile 16-bit TN GEMM with direct global -> LDS loads.
+//
+// 256x256 block tile, BK = 64, 8 waves (2 x 4, each 128x64), two LDS stages
+// of 64 KB.  global_load_lds_dwordx4 writes each lane's 16 bytes to
+// LDS base + 16*lane, so one wave instruction fills 1 KB = 8 tile rows of
+// 128 bytes; which global chunk a lane fetches is free, and it is chosen so
+// the LDS rows are XOR-swizzled (physical chunk = logical chunk ^ (row & 7)),
+// making the 16-byte fragment reads conflict-free without padding.  No
+// staging registers and no LDS store instructions: the freed registers
+// double-buffer the MFMA fragments, so each k-step's LDS reads are issued
+// one step ahead of its MFMAs.  Stage k+1 is loaded while stage k is
+// computed; one wait + barrier per stage.
+// ---------------------------------------------------------------------------
+template <typename T, int WM, int WN, typename Epi>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uint16_t* __restrict__ A,
+                                                                         const uint16_t* __restrict__ Bt, int M,
+                                                                         int N, int K, int lda, int ldb, int tiles_n,
+                                                                         Epi epi) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int NW = WM * WN;        // waves
+  constexpr int LPW = 32 / NW;       // 1 KB load instructions per wave per operand
+  constexpr int TM = BM / WM / 32;
+  constexpr int TN = BN / WN / 32;
+  constexpr int ROWB = BK * 2;      // bytes per LDS row (128)
+  constexpr int STAGE = (BM + BN) * BK;  // elements per stage
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = (wave / WN) * (BM / WM);
+  const int wn = (wave % WN) * (BN / WN);
+
+  constexpr int GROUP = 8;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int nwg = gridDim.x;
+  const int full = nwg & ~7;
+  int pid = blockIdx.x;
+  if (pid < full) {
+    pid = (pid & 7) * (full >> 3) + (pid >> 3);
+  }
+  const int group_size = GROUP * tiles_n;
+  const int group = pid / group_size;
+  const int first_m = group * GROUP;
+  const int gm = min(tiles_m - first_m, GROUP);
+  const int in_group = pid - group * group_size;
+  const int bm = (first_m + in_group % gm) * BM;
+  const int bn = (in_group / gm) * BN;
+
+  // Load mapping: instruction i (of 32 per operand) fills tile rows 8i..8i+7;
+  // wave w issues i = NW*j + w, j = 0 .. 32/NW - 1.  Lane l -> row 8i + l/8, physical
+  // chunk l%8, logical chunk (l%8) ^ (row & 7).
+  const int lrow8 = lane >> 3;
+  const int pchunk = lane & 7;
+  const uint16_t* a_src[LPW];
+  const uint16_t* b_src[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int row = 8 * (NW * j + wave) + lrow8;
+    const int lchunk = pchunk ^ (row & 7);
+    a_src[j] = A + static_cast<size_t>(bm + row) * lda + lchunk * 8;
+    b_src[j] = Bt + static_cast<size_t>(bn + row) * ldb + lchunk * 8;
+  }
+  auto issue = [&](int buf, int k0) {
+    uint16_t* base = smem + buf * STAGE;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      load_lds16(a_src[j] + k0, base + (NW * j + wave) * 8 * BK);
+    }
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      load_lds16(b_src[j] + k0, base + BM * BK + (NW * j + wave) * 8 * BK);
+    }
+  };
+
+  // Fragment read: row r, logical chunk c -> byte r*128 + ((c ^ (r&7)) * 16).
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  auto frag = [&](const uint16_t* base, int row, int c) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + row * ROWB +
+                                           ((c ^ (row & 7)) << 4));
+  };
+
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      acc[i][j] = zero16();
+    }
+  }
+
+  const int nk = K / BK;
+  issue(0, 0);
+  __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0); expcnt / lgkmcnt left at their maxima
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < nk) {
+      issue(buf ^ 1, (kt + 1) * BK);
+    }
+    const uint16_t* As = smem + buf * STAGE;
+    const uint16_t* Bs = As + BM * BK;
+    u32x4 af[2][TM];
+    u32x4 bf[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      af[0][i] = frag(As, wm + i * 32 + lrow, lhalf);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      bf[0][j] = frag(Bs, wn + j * 32 + lrow, lhalf);
+    }
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          af[cur ^ 1][i] = frag(As, wm + i * 32 + lrow, 2 * (s + 1) + lhalf);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          bf[cur ^ 1][j] = frag(Bs, wn + j * 32 + lrow, 2 * (s + 1) + lhalf);
+        }
+      }
+      // Keep the next step's LDS reads ahead of this step's MFMAs (the
+      // scheduler would otherwise sink them next to their use and expose the
+      // full LDS latency before every MFMA group).
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          acc[i][j] = mfma32x32x16<T>(af[cur][i], bf[cur][j], acc[i][j]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // this wave's loads of stage kt+1 have landed
+    stage_barrier();                      // everyone's have; everyone is done with stage kt
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = bn + wn + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = bm + wm + i * 32 + acc_row(r, lane);
+        if (m < M && n < N) {
+          epi(m, n, acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// Tile configurations (block tile BM x BN, waves WM x WN, BK = 64):
+//   lds    256x256, 8 waves 2x4 (128x64 each), global -> LDS direct loads
+//          (gemm_half_tn_lds_kernel); needs A / Bt padded to 256 rows
+//   big8   256x256, 8 waves 2x4, LDS double buffer fed from registers
+//   big4   256x256, 4 waves 2x2 (128x128 each), 1 wave / SIMD
+//   mid    128x128, 4 waves 2x2 (64x64 each)
+//   small   64x64,  4 waves 2x2 (32x32 each)
+// Default: the largest tile that still gives at least one workgroup per CU
+// (lds where the operands are padded, big8 elsewhere).
+// CJ_HIP_GEMM_TILE=<name> overrides the choice (tuning sweeps), like the
+// reference's CJ_* tuning variables.
+enum class HalfTile { kLds, kBig8, kBig4, kMid, kSmall };
 
 inline int tiles_for(int M, int N, int b) { return ((M + b - 1) / b) * ((N + b - 1) / b); }
 
-inline HalfTile pick_half_tile(int M, int N) {
+inline HalfTile pick_half_tile(int M, int N, bool padded) {
+  if (const char* env = getenv("CJ_HIP_GEMM_TILE")) {
+    const std::string v(env);
+    if (v == "lds" && padded) return HalfTile::kLds;
+    if (v == "big8") return HalfTile::kBig8;
+    if (v == "big4") return HalfTile::kBig4;
+    if (v == "mid") return HalfTile::kMid;
+    if (v == "small") return HalfTile::kSmall;
+  }
   constexpr int kCUs = 256;
   if (tiles_for(M, N, 256) >= kCUs) {
-    return HalfTile::kBig;
+    return padded ? HalfTile::kLds : HalfTile::kBig8;
   }
   if (tiles_for(M, N, 128) >= kCUs) {
     return HalfTile::kMid;
@@ -544,12 +751,12 @@ inline HalfTile pick_half_tile(int M, int N) {
   return HalfTile::kSmall;
 }
 
-template <typename T, int BM, int BN, int WM, int WN, typename LoadA, typename Epi>
+template <typename T, int BM, int BN, int WM, int WN, typename LoadA, typename Epi, int STORE_AT = 32, int BK = kHBK>
 static hipError_t launch_gemm_half_cfg(LoadA load_a, const uint16_t* Bt, int M, int N, int K, int ldb, Epi epi,
                                        hipStream_t stream) {
   const int tiles_m = (M + BM - 1) / BM;
   const int tiles_n = (N + BN - 1) / BN;
-  hipLaunchKernelGGL((gemm_half_tn_kernel<T, BM, BN, kHBK, WM, WN, LoadA, Epi>), dim3(tiles_m * tiles_n),
+  hipLaunchKernelGGL((gemm_half_tn_kernel<T, BM, BN, BK, WM, WN, STORE_AT, LoadA, Epi>), dim3(tiles_m * tiles_n),
                      dim3(WM * WN * 64), 0, stream, load_a, Bt, M, N, K, ldb, tiles_n, epi);
   return hipGetLastError();
 }
@@ -557,15 +764,28 @@ static hipError_t launch_gemm_half_cfg(LoadA load_a, const uint16_t* Bt, int M, 
 template <typename T, typename LoadA, typename Epi>
 static hipError_t launch_gemm_half(LoadA load_a, const uint16_t* Bt, int M, int N, int K, int ldb, Epi epi,
                                    hipStream_t stream) {
-  switch (pick_half_tile(M, N)) {
-    case HalfTile::kBig:
+  switch (pick_half_tile(M, N, false)) {
+    case HalfTile::kLds:
+    case HalfTile::kBig8:
       return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
+    case HalfTile::kBig4:
+      return launch_gemm_half_cfg<T, 256, 256, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
     case HalfTile::kMid:
       return launch_gemm_half_cfg<T, 128, 128, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
     case HalfTile::kSmall:
     default:
       return launch_gemm_half_cfg<T, 64, 64, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
   }
+}
+
+template <typename T, int WM, int WN>
+static hipError_t launch_gemm_lds(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda,
+                                  int ldb, int ldc, hipStream_t stream) {
+  const int tiles_n = (N + 255) / 256;
+  const dim3 grid(((M + 255) / 256) * tiles_n);
+  hipLaunchKernelGGL((gemm_half_tn_lds_kernel<T, WM, WN, EpiF32>), grid, dim3(WM * WN * 64), 0, stream, A, Bt, M, N,
+                     K, lda, ldb, tiles_n, EpiF32{C, ldc});
+  return hipGetLastError();
 }
 
 }  // namespace lchip::k
@@ -589,14 +809,22 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
   if (K % kHBK != 0) {
     return hipErrorInvalidValue;
   }
+  // A and Bt come from the resident upload, padded to 256 rows.
+  if (M > 16 && K > 0 && pick_half_tile(M, N, true) == HalfTile::kLds) {
+    return t == Half::kBF16 ? launch_gemm_lds<BF16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
+                            : launch_gemm_lds<F16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
+  }
   if (M <= 16) {
     // Bt must be readable up to roundup(N, 32) rows (callers pad to 256).
     constexpr int NT = 2;
+    constexpr int WAVES = 4;
     const dim3 grid((N + 16 * NT - 1) / (16 * NT));
     if (t == Half::kBF16) {
-      hipLaunchKernelGGL((gemm_skinny_kernel<BF16, NT>), grid, dim3(256), 0, stream, A, Bt, C, M, N, K, lda, ldb, ldc);
+      hipLaunchKernelGGL((gemm_skinny_kernel<BF16, NT, WAVES>), grid, dim3(WAVES * 64), 0, stream, A, Bt, C, M, N, K,
+                         lda, ldb, ldc);
     } else {
-      hipLaunchKernelGGL((gemm_skinny_kernel<F16, NT>), grid, dim3(256), 0, stream, A, Bt, C, M, N, K, lda, ldb, ldc);
+      hipLaunchKernelGGL((gemm_skinny_kernel<F16, NT, WAVES>), grid, dim3(WAVES * 64), 0, stream, A, Bt, C, M, N, K,
+                         lda, ldb, ldc);
     }
     return hipGetLastError();
   }

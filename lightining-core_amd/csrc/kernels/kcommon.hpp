@@ -26,14 +26,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 struct BF16 {};
 struct F16 {};
 
-// fp32 -> bf16 bits, round to nearest even (NaN -> canonical quiet NaN).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// fp32 -> bf16 bits, round to nearest even (gfx950 v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) {
-    return 0x7fc0u;
-  }
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 // fp32 -> fp16 bits, round to nearest even (hardware conversion).
@@ -57,6 +54,13 @@ __device__ __forceinline__ uint16_t to_half_bits<F16>(float f) {
 template <typename T>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
   return static_cast<uint32_t>(to_half_bits<T>(lo)) | (static_cast<uint32_t>(to_half_bits<T>(hi)) << 16);
+}
+template <>
+__device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
+  bf16x2 v;
+  v[0] = static_cast<__bf16>(lo);
+  v[1] = static_cast<__bf16>(hi);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // 32x32x16 MFMA on 8 packed 16-bit values per lane (as four dwords).

@@ -73,11 +73,22 @@ TuneEntry gemmConfig(const MatMulResident& r) {
     e.waves = 4;
     e.split_k = 4;
   } else {
+    // mirrors pick_half_tile() in kernels/gemm.hip
+    const auto tiles = [&](std::size_t b) { return ((r.m + b - 1) / b) * ((r.n + b - 1) / b); };
     e.kernel = "half_tn_32x32x16";
-    e.tile_m = 128;
-    e.tile_n = 128;
-    e.tile_k = 64;
-    e.waves = 4;
+    if (tiles(256) >= 256) {
+      e.tile_m = e.tile_n = 256;
+      e.tile_k = 64;
+      e.waves = 8;
+    } else if (tiles(128) >= 256) {
+      e.tile_m = e.tile_n = 128;
+      e.tile_k = 64;
+      e.waves = 4;
+    } else {
+      e.tile_m = e.tile_n = 64;
+      e.tile_k = 64;
+      e.waves = 4;
+    }
   }
   return e;
 }

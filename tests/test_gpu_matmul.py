@@ -144,3 +144,25 @@ def test_trace_records_hip_dispatch(lc):
     assert ev and ev[-1]["op"] == "matmul"
     assert ev[-1]["requested"] == "hip" and ev[-1]["selected"] == "hip" and not ev[-1]["fallback"]
     assert ev[-1]["size_bytes"] == 4 * 7 * 5
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+def test_upload_rounding_bitexact(lc, dtype):
+    # A . I with one nonzero per output sum is exact in fp32, so C equals the
+    # device-rounded A bit for bit: the upload conversion must match the
+    # round-to-nearest-even of lightning_core.synth (ties, tiny, large values).
+    m, k = 16, 64
+    rng = np.random.default_rng(5)
+    base = rng.standard_normal((m, k)).astype(np.float32)
+    bits = base.view(np.uint32)
+    bits[0, :32] = (bits[0, :32] & 0xFFFF0000) | 0x8000  # exact bf16 ties
+    bits[1, :32] = (bits[1, :32] & 0xFFFFE000) | 0x1000  # exact fp16 ties (normal range)
+    base[2, :8] = [1e-30, -1e-30, 3e38, -3e38, 6e-5, 65504.0, 1e-8, 0.0]
+    if dtype == "f16":
+        base[2, 2:4] = [60000.0, -60000.0]
+    s = lc.MatMulResidentSession(m, k, k, dtype)
+    s.start_into(base, np.eye(k, dtype=np.float32))
+    got = s.finish_into().reshape(m, k)
+    exp = synth.round_to(base, dtype)
+    # values, not bit patterns: a rounded -0.0 sums to +0.0 in the accumulator
+    np.testing.assert_array_equal(got, exp)
