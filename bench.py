@@ -162,7 +162,7 @@ def bench_config2(lc, synth, steps, warmup, cpu):
     kms = timed(lc, lambda it: sess[0].run_batch_sync_cached_no_download(it), reps) / reps
     kflops = 2.0 * 1024 ** 3
     achieved = kflops / (kms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "gemm_f32_kernel (1024^3, v_mfma_f32_32x32x2_f32)",
+    roofline = {"bound": "mfma", "kernel": "gemm_f32_lds_kernel (1024^3, v_mfma_f32_32x32x2_f32)",
                 "achieved": round(achieved, 3), "peak": PEAK_TFLOPS["f32"], "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_TFLOPS["f32"], 4), "traffic": None,
                 "avg_kernel_ms": round(kms, 5), "algorithmic_flops_per_launch": int(kflops)}

@@ -17,10 +17,26 @@ constexpr int kHalfGemmBN = 256;  // rows of Bt a half-GEMM block may read
 constexpr int kHalfGemmBK = 64;   // K must be a multiple of this (zero-padded)
 constexpr int kAttnQBlock = 128;  // queries per attention workgroup; S_pad multiple
 
+constexpr int kF32GemmBM = 64;    // fp32 padded GEMM: rows of A a block reads
+constexpr int kF32GemmBN = 64;    // columns of B a block reads
+constexpr int kF32GemmBK = 64;    // K multiple (zero-padded)
+
 // ---- fp32 ------------------------------------------------------------------
 // C[M,N] = A[M,K] . B[K,N] (row-major, leading dimensions lda/ldb/ldc), any sizes.
 hipError_t gemmF32(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
                    hipStream_t stream);
+// Same product on padded operands: A [roundup(M,64), K] (lda), B [K,
+// roundup(N,64)] (ldb), K a multiple of kF32GemmBK, pads zero, lda/ldb
+// multiples of 4 and both bases 16-byte aligned.  C [M, N] (ldc).  Stream-K
+// over at most max_groups workgroups: `part` holds max_groups * 4096 floats
+// of partial tiles and `flags` max_groups ints, zero before the first call
+// (each call leaves them zero).  Calls that share part/flags must not overlap.
+hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
+                         float* part, int* flags, int max_groups, hipStream_t stream);
+// dst[r][c] = src[r][c] (row stride ld_src) for r < rows, c < cols; 0 up to
+// rows_pad x cols_pad (dst row stride cols_pad).
+hipError_t padCopyF32(const float* src, float* dst, int rows, int cols, size_t ld_src, int rows_pad, int cols_pad,
+                      hipStream_t stream);
 // out2d = cols[M,K] . Wt^T where Wt is [N,K] (conv weights as stored, OIHW);
 // epilogue adds bias, applies ReLU and scatters to NCHW out[img, n, pix]
 // (m = img*ohw + pix).

@@ -41,6 +41,26 @@ __global__ __launch_bounds__(256) void convert_pad_kernel(const float* __restric
   }
 }
 
+__global__ __launch_bounds__(256) void pad_copy_f32_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                           int rows, int cols, size_t ld_src, int rows_pad,
+                                                           int cols_pad) {
+  // 4 output elements per thread along the padded row; cols_pad % 4 == 0.
+  const int c4 = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (c4 >= cols_pad) {
+    return;
+  }
+  for (int r = blockIdx.y; r < rows_pad; r += gridDim.y) {
+    float4 v;
+    float* pv = reinterpret_cast<float*>(&v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int c = c4 + j;
+      pv[j] = (r < rows && c < cols) ? src[static_cast<size_t>(r) * ld_src + c] : 0.0f;
+    }
+    *reinterpret_cast<float4*>(dst + static_cast<size_t>(r) * cols_pad + c4) = v;
+  }
+}
+
 // dst[c][r] = half(src[r][c]); block = 32 (r) x 64 (c) tile.
 template <typename T>
 __global__ __launch_bounds__(256) void convert_transpose_pad_kernel(const float* __restrict__ src,
@@ -146,6 +166,17 @@ hipError_t convertPad(const float* src, uint16_t* dst, int batch, int rows, int 
     hipLaunchKernelGGL((convert_pad_kernel<F16>), grid, dim3(256), 0, stream, src, dst, rows, cols, ld_src, rows_pad,
                        cols_pad, src_bstride, dst_bstride);
   }
+  return hipGetLastError();
+}
+
+hipError_t padCopyF32(const float* src, float* dst, int rows, int cols, size_t ld_src, int rows_pad, int cols_pad,
+                      hipStream_t stream) {
+  if (rows_pad <= 0 || cols_pad <= 0 || cols_pad % 4 != 0 || rows > rows_pad || cols > cols_pad) {
+    return hipErrorInvalidValue;
+  }
+  const dim3 grid((cols_pad + 1023) / 1024, rows_pad < 65535 ? rows_pad : 65535);
+  hipLaunchKernelGGL(pad_copy_f32_kernel, grid, dim3(256), 0, stream, src, dst, rows, cols, ld_src, rows_pad,
+                     cols_pad);
   return hipGetLastError();
 }
 

@@ -544,6 +544,17 @@ constexpr int kHBK = 64;
 __device__ __forceinline__ void load_lds16(const uint16_t* src, uint16_t* lds_base) {
   __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
 }
+__device__ __forceinline__ void load_lds16(const float* src, float* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) for the small n the pipelines use (expcnt / lgkmcnt
+// left at their maxima; vmcnt's low four bits sit in bits 3:0).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | N);
+}
 
 // Workgroup barrier without the release fence of __syncthreads(): the fence
 // would make the compiler drain every outstanding global -> LDS load
@@ -564,8 +575,12 @@ __device__ __forceinline__ void stage_barrier() {
 // of 64 KB.  global_load_lds_dwordx4 writes each lane's 16 bytes to
 // LDS base + 16*lane, so one wave instruction fills 1 KB = 8 tile rows of
 // 128 bytes; which global chunk a lane fetches is free, and it is chosen so
-// the LDS rows are XOR-swizzled (physical chunk = logical chunk ^ (row & 7)),
-// making the 16-byte fragment reads conflict-free without padding.  No
+// the LDS rows are XOR-swizzled (physical chunk = logical chunk ^
+// ((row >> 1) & 7)).  gfx950's LDS serves a 16-byte read for 16 lanes per
+// clock (256 bytes, 64 banks); a fragment read puts 16 consecutive rows of
+// one logical chunk in such a group, and with 128-byte rows even and odd rows
+// land in opposite bank halves, so the swizzle only has to separate the 8
+// even (and 8 odd) rows: conflict-free without padding.  No
 // staging registers and no LDS store instructions: the freed registers
 // double-buffer the MFMA fragments, so each k-step's LDS reads are issued
 // one step ahead of its MFMAs.  Stage k+1 is loaded while stage k is
@@ -609,7 +624,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
 
   // Load mapping: instruction i (of 32 per operand) fills tile rows 8i..8i+7;
   // wave w issues i = NW*j + w, j = 0 .. 32/NW - 1.  Lane l -> row 8i + l/8, physical
-  // chunk l%8, logical chunk (l%8) ^ (row & 7).
+  // chunk l%8, logical chunk (l%8) ^ ((row >> 1) & 7).
   const int lrow8 = lane >> 3;
   const int pchunk = lane & 7;
   const uint16_t* a_src[LPW];
@@ -617,7 +632,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int row = 8 * (NW * j + wave) + lrow8;
-    const int lchunk = pchunk ^ (row & 7);
+    const int lchunk = pchunk ^ ((row >> 1) & 7);
     a_src[j] = A + static_cast<size_t>(bm + row) * lda + lchunk * 8;
     b_src[j] = Bt + static_cast<size_t>(bn + row) * ldb + lchunk * 8;
   }
@@ -638,7 +653,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
   const int lhalf = lane >> 5;
   auto frag = [&](const uint16_t* base, int row, int c) -> u32x4 {
     return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + row * ROWB +
-                                           ((c ^ (row & 7)) << 4));
+                                           ((c ^ ((row >> 1) & 7)) << 4));
   };
 
   floatx16 acc[TM][TN];
@@ -714,6 +729,303 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
         }
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 GEMM on padded operands: direct global -> LDS loads, stream-K.
+//
+// 64x64 block tile, 4*KS waves: each group of 4 waves covers the four 32x32
+// output sub-tiles on its 1/KS of every K stage (KS waves per SIMD, so one
+// wave's LDS waits hide behind the others' MFMAs); the KS parts are summed
+// through LDS at the end of a tile.  BK = 32 or 64 per
+// stage, STAGES buffers, loads issued STAGES-1 stages ahead, one wait +
+// barrier per stage.
+//
+// LDS: A stage [64 m][BK k] with the 16-byte chunks of each row XOR-swizzled
+// (by row & 15 for 256-byte rows, (row >> 1) & 7 for 128-byte rows), so the
+// 16 rows one 16-byte read serves per clock (256 bytes, 64 banks) hit 16
+// different bank groups; B stage [BK k][64 n] with the two 128-byte halves of
+// every row that has bit 2 set swapped.  v_mfma_f32_32x32x2_f32 takes one k
+// pair per lane half; with the k permutation "MFMA j of an 8-k group uses
+// k = 8c + j (lanes 0-31) and 8c + 4 + j (lanes 32-63)", a lane's four A
+// values of a group are one 16-byte LDS read, and its B values are four
+// 4-byte reads in which the two half-waves (rows 4 apart) use opposite bank
+// halves.
+//
+// Work split (stream-K): the T*nk (tile, k-stage) iterations are divided
+// evenly over the G workgroups, workgroup w taking [w*I/G, (w+1)*I/G).  A
+// workgroup walks its range downwards, so the first segment it finishes is
+// the low-k part of its last tile and the last segment the high-k part of
+// its first tile.  A segment without the tile's last k stage publishes its
+// partial tile (part[w], flag[w] = 1) as soon as it is done; the segment
+// holding the last stage owns the tile: it waits for the flags of the lower
+// workgroups that hold the rest, adds their partials in workgroup order
+// (deterministic) and stores.  Waits only ever target lower workgroup ids,
+// which the in-order dispatch has already started, and each spin is bounded,
+// so every wave exits.  With T a multiple of G (1024^3: 256 tiles on 256
+// CUs) every range is whole tiles and nothing is published.  The owner
+// clears the flags it consumed, so they are zero again when the kernel ends.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
+  stage_barrier();
+}
+
+template <int BK, int STAGES, int KS, bool SK, typename Epi>
+__global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                           int M, int N, int lda, int ldb, int tiles_m, int tiles_n,
+                                                           int nk, float* __restrict__ part, int* __restrict__ flags,
+                                                           Epi epi) {
+  constexpr int BM = 64, BN = 64;
+  constexpr int A_STAGE = BM * BK;            // floats
+  constexpr int STAGE = (BM + BN) * BK;       // floats
+  constexpr int ACH = BK / 4;                 // 16-byte chunks per A row
+  constexpr int A_RPI = 64 / ACH;             // A rows per 1 KB load instruction
+  constexpr int NW = 4 * KS;                  // waves
+  constexpr int LPW = BK / 4 / NW;            // load instructions per wave per operand per stage
+  constexpr int GPW = BK / 8 / KS;            // 8-k groups per wave per stage
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(LPW >= 1 && (BK / 4) % NW == 0 && GPW >= 1, "K split");
+  __shared__ __attribute__((aligned(16))) float smem[STAGES * STAGE + (KS - 1) * 4096];
+  auto swz = [](int row) { return ACH == 16 ? (row & 15) : ((row >> 1) & 7); };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int sub = wave & 3;
+  const int kh = wave >> 2;
+  const int wm = (sub >> 1) * 32;
+  const int wn = (sub & 1) * 32;
+
+  const int G = gridDim.x;
+  const int w = blockIdx.x;
+  const int T = tiles_m * tiles_n;
+  const long long I = static_cast<long long>(T) * nk;
+  auto begin_of = [&](int q) { return static_cast<int>(static_cast<long long>(q) * I / G); };
+  // !SK: one whole tile per workgroup (G == T), no partials.
+  const int it0 = SK ? begin_of(w) : w * nk;
+  const int it1 = SK ? begin_of(w + 1) : it0 + nk;
+  const int n_it = it1 - it0;
+  if (n_it <= 0) {
+    return;
+  }
+
+  // Tile t -> (bm, bn).  XCD-aware: consecutive tile ids (consecutive
+  // workgroups) land on different XCDs, so pid = (t % 8) * (T / 8) + t / 8
+  // gives each XCD a contiguous pid range, walked in groups of 8 tile rows.
+  auto origin = [&](int t, int& bm, int& bn) {
+    const int full = T & ~7;
+    int pid = t;
+    if (pid < full) {
+      pid = (pid & 7) * (full >> 3) + (pid >> 3);
+    }
+    const int group_size = 8 * tiles_n;
+    const int group = pid / group_size;
+    const int first_m = group * 8;
+    const int gm = min(tiles_m - first_m, 8);
+    const int in_group = pid - group * group_size;
+    bm = (first_m + in_group % gm) * BM;
+    bn = (in_group / gm) * BN;
+  };
+
+  // Wave w issues A instructions w + NW*j (A_RPI rows each) and B
+  // instructions w + NW*j (4 k-rows of 256 bytes each), j < LPW; offsets
+  // within a tile.
+  const float* a_src[LPW];
+  const float* b_src[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int ins = wave + NW * j;
+    const int row = A_RPI * ins + lane / ACH;
+    const int lch = (lane % ACH) ^ swz(row);
+    a_src[j] = A + static_cast<size_t>(row) * lda + lch * 4;
+    const int krow = 4 * ins + (lane >> 4);
+    b_src[j] = B + static_cast<size_t>(krow) * ldb + ((lane & 15) ^ (krow & 4 ? 8 : 0)) * 4;
+  }
+  // Issue cursor: next (tile, k) to load, walking down from it1 - 1.
+  int is_t = (it1 - 1) / nk;
+  int is_k = (it1 - 1) - is_t * nk;
+  int is_bm, is_bn;
+  origin(is_t, is_bm, is_bn);
+  auto issue_next = [&](int buf) {
+    float* base = smem + buf * STAGE;
+    const size_t aoff = static_cast<size_t>(is_bm) * lda + is_k * BK;
+    const size_t boff = static_cast<size_t>(is_k) * BK * ldb + is_bn;
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      load_lds16(a_src[j] + aoff, base + (wave + NW * j) * 256);
+      load_lds16(b_src[j] + boff, base + A_STAGE + (wave + NW * j) * 256);
+    }
+    if (--is_k < 0) {
+      is_k = nk - 1;
+      if (--is_t >= 0) {
+        origin(is_t, is_bm, is_bn);
+      }
+    }
+  };
+
+  floatx16 acc0 = zero16();
+  floatx16 acc1 = zero16();
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) {
+    if (s < n_it) {
+      issue_next(s);
+    }
+  }
+  const int arow = wm + (lane & 31);
+  const int half = lane >> 5;
+  float* red = smem + STAGES * STAGE + sub * 1024 + lane;
+
+  // Segment end: sum the K parts, then publish, or own and store.
+  auto finish = [&](int t, bool has_first, bool has_last) {
+    if (kh > 0) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        red[(kh - 1) * 4096 + i * 64] = acc0[i] + acc1[i];
+      }
+    }
+    lds_barrier();
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      v[i] = acc0[i] + acc1[i];
+#pragma unroll
+      for (int q = 0; q < KS - 1; ++q) {
+        v[i] += red[q * 4096 + i * 64];
+      }
+    }
+    // Partials and flags move with device-scope (sc1) loads and stores,
+    // which are coherent across the XCDs' L2s by themselves; a release /
+    // acquire fence instead would write back and invalidate the whole L2 of
+    // the XCD and cost every other workgroup there its cached A / B tiles.
+    // Order comes from waiting for the partial stores to complete (vmcnt)
+    // before the flag store, and from the barrier after the flag spin.
+    float* mine = part + static_cast<size_t>(w) * 4096 + sub * 1024 + lane;
+    if (!has_last) {
+      if (kh == 0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          __hip_atomic_store(mine + i * 64, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      wait_vmcnt<0>();
+      stage_barrier();
+      if (tid == 0) {
+        __hip_atomic_store(flags + w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      return;
+    }
+    if (!has_first) {
+      int wf = static_cast<int>(static_cast<long long>(t) * nk * G / I);
+      while (wf + 1 < G && begin_of(wf + 1) <= t * nk) {
+        ++wf;
+      }
+      while (wf > 0 && begin_of(wf) > t * nk) {
+        --wf;
+      }
+      if (tid == 0) {
+        for (int q = wf; q < w; ++q) {
+          if (begin_of(q) == begin_of(q + 1)) {
+            continue;
+          }
+          for (int spin = 0; spin < (1 << 22); ++spin) {
+            if (__hip_atomic_load(flags + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+              break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+          }
+        }
+      }
+      stage_barrier();
+      if (kh == 0) {
+        for (int q = wf; q < w; ++q) {
+          float* theirs = part + static_cast<size_t>(q) * 4096 + sub * 1024 + lane;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            v[i] += __hip_atomic_load(theirs + i * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+      }
+      if (tid == 0) {
+        for (int q = wf; q < w; ++q) {
+          __hip_atomic_store(flags + q, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    if (kh == 0) {
+      int bm, bn;
+      origin(t, bm, bn);
+      const int n = bn + wn + (lane & 31);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int m = bm + wm + acc_row(i, lane);
+        if (m < M && n < N) {
+          epi(m, n, v[i]);
+        }
+      }
+    }
+  };
+
+  int ct = (it1 - 1) / nk;
+  int ck = (it1 - 1) - ct * nk;
+  bool seg_has_last = ck == nk - 1;
+  for (int j = 0; j < n_it; ++j) {
+    // Stage j's loads (own) have landed once at most min(n_it-1-j, STAGES-2)
+    // later stages are outstanding; the barrier extends that to every wave
+    // and retires the reads of stage j-1, whose buffer is refilled next.
+    const int later = min(n_it - 1 - j, STAGES - 2);
+    if (later >= 2) {
+      wait_vmcnt<4 * LPW>();
+    } else if (later == 1) {
+      wait_vmcnt<2 * LPW>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    stage_barrier();
+    if (j + STAGES - 1 < n_it) {
+      issue_next((j + STAGES - 1) % STAGES);
+    }
+    const float* As = smem + (j % STAGES) * STAGE;
+    const float* Bs = As + A_STAGE;
+    floatx4 a[GPW];
+    float b[GPW][4];
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      const int c = kh * GPW + g;
+      const int lch = 2 * c + half;
+      a[g] = *reinterpret_cast<const floatx4*>(As + arow * BK + ((lch ^ swz(arow)) << 2));
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        b[g][q] = Bs[(8 * c + 4 * half + q) * BN + ((wn + (lane & 31)) ^ (half << 5))];
+      }
+    }
+    // All of the stage's fragment reads go out before its first MFMA (the
+    // scheduler would otherwise pair each group's reads with its MFMAs and
+    // expose the LDS latency once per group).
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 0; g < GPW; ++g) {
+      acc0 = mfma32x32x2f32(a[g][0], b[g][0], acc0);
+      acc1 = mfma32x32x2f32(a[g][1], b[g][1], acc1);
+      acc0 = mfma32x32x2f32(a[g][2], b[g][2], acc0);
+      acc1 = mfma32x32x2f32(a[g][3], b[g][3], acc1);
+    }
+    if constexpr (SK) {
+      if (ck == 0 || j == n_it - 1) {
+        finish(ct, ck == 0, seg_has_last);
+        acc0 = zero16();
+        acc1 = zero16();
+        seg_has_last = true;
+      }
+      if (--ck < 0) {
+        ck = nk - 1;
+        --ct;
+      }
+    }
+  }
+  if constexpr (!SK) {
+    finish(w, true, true);
   }
 }
 
@@ -797,6 +1109,42 @@ using namespace lchip::k;
 hipError_t gemmF32(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
                    hipStream_t stream) {
   return launch_gemm_f32<false>(A, B, M, N, K, lda, ldb, EpiStoreF32{C, ldc}, stream);
+}
+
+hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
+                         float* part, int* flags, int max_groups, hipStream_t stream) {
+  if (K <= 0 || K % kF32GemmBK != 0 || lda % 4 != 0 || ldb % 4 != 0 || M <= 0 || N <= 0 || max_groups <= 0) {
+    return hipErrorInvalidValue;
+  }
+  const int tiles_m = (M + 63) / 64;
+  const int tiles_n = (N + 63) / 64;
+  const char* env = getenv("CJ_HIP_GEMM_F32");
+  const std::string v = env != nullptr ? env : "";
+  const int bk = v == "bk32" ? 32 : 64;
+  const int nk = K / bk;
+  const int tiles = tiles_m * tiles_n;
+  // Whole tiles per workgroup when they fill the CUs evenly (or there are
+  // many of them); stream-K otherwise.
+  const bool sk = v == "sk" || (v != "dp" && tiles % max_groups != 0 && tiles < 8 * max_groups);
+  const long long iters = static_cast<long long>(tiles) * nk;
+  const int groups = sk ? static_cast<int>(iters < max_groups ? iters : max_groups) : tiles;
+  const EpiStoreF32 epi{C, ldc};
+  if (v == "bk32") {
+    if (sk) {
+      hipLaunchKernelGGL((gemm_f32_lds_kernel<32, 4, 2, true, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A,
+                         B, M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
+    } else {
+      hipLaunchKernelGGL((gemm_f32_lds_kernel<32, 4, 2, false, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A,
+                         B, M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
+    }
+  } else if (sk) {
+    hipLaunchKernelGGL((gemm_f32_lds_kernel<64, 4, 2, true, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A, B,
+                       M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
+  } else {
+    hipLaunchKernelGGL((gemm_f32_lds_kernel<64, 4, 2, false, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A, B,
+                       M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
+  }
+  return hipGetLastError();
 }
 
 hipError_t gemmF32ConvNchw(const float* cols, const float* Wt, float* out, int M, int N, int K, const float* bias,

@@ -69,23 +69,6 @@ void traceOpDispatch(TraceOp op, Device requested, Device selected, bool fallbac
 int encodeDispatch(Device requested, Device selected, bool fallback);
 
 // ---- HIP device context --------------------------------------------------------
-// One context per process for the single visible gfx950 device: one
-// non-blocking stream (default priority) that every kernel, copy and event of
-// the library uses, and one mutex that serialises host-side use of shared
-// buffers (the reference serialises its attention backend the same way,
-// src/attention_metal.mm:1855).
-struct HipContext {
-  std::recursive_mutex mu;
-  int device = 0;
-  hipStream_t stream = nullptr;
-  hipDeviceProp_t props{};
-};
-
-bool hipAvailable();
-// Returns the context, or nullptr with the status set (kNotSupported when no
-// gfx950 device is visible).
-HipContext* hipContext(Status* st);
-
 // Device allocation that grows (1.5x, like the reference's Metal buffers,
 // src/attention_metal.mm:150-164) and never shrinks.  Contents are not kept
 // across growth.  Freed by reset() or the destructor.
@@ -108,6 +91,27 @@ class DeviceBuffer {
   void* ptr_ = nullptr;
   std::size_t bytes_ = 0;
 };
+
+// One context per process for the single visible gfx950 device: one
+// non-blocking stream (default priority) that every kernel, copy and event of
+// the library uses, and one mutex that serialises host-side use of shared
+// buffers (the reference serialises its attention backend the same way,
+// src/attention_metal.mm:1855).
+struct HipContext {
+  std::recursive_mutex mu;
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipDeviceProp_t props{};
+  // Stream-K workspace of the fp32 GEMM (partial tiles + ready flags), one
+  // slot per workgroup; used by launches on `stream` only, so never shared
+  // by two kernels at once.
+  DeviceBuffer gemm_part, gemm_flags;
+};
+
+bool hipAvailable();
+// Returns the context, or nullptr with the status set (kNotSupported when no
+// gfx950 device is visible).
+HipContext* hipContext(Status* st);
 
 // Upload / download on the context stream (pageable host memory).
 Status upload(HipContext* ctx, void* dst, const void* src, std::size_t bytes);

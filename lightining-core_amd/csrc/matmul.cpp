@@ -24,8 +24,16 @@ namespace {
 
 Status uploadA(HipContext* ctx, MatMulResident& r, const float* a) {
   if (!isHalf(r.dtype)) {
-    LC_TRY(r.a.ensure(r.m * r.k * sizeof(float)));
-    return upload(ctx, r.a.get(), a, r.m * r.k * sizeof(float));
+    // fp32: A [roundup(M, 64), roundup(K, 64)], zero pads
+    const std::size_t mp = roundUp(r.m, kern::kF32GemmBM);
+    const std::size_t kp = roundUp(r.k, kern::kF32GemmBK);
+    LC_TRY(r.stage.ensure(r.m * r.k * sizeof(float)));
+    LC_TRY(r.a.ensure(mp * kp * sizeof(float)));
+    LC_TRY(upload(ctx, r.stage.get(), a, r.m * r.k * sizeof(float)));
+    const hipError_t e = kern::padCopyF32(r.stage.as<float>(), r.a.as<float>(), static_cast<int>(r.m),
+                                          static_cast<int>(r.k), r.k, static_cast<int>(mp), static_cast<int>(kp),
+                                          ctx->stream);
+    return e == hipSuccess ? Status::kSuccess : failHip(e, "matmul upload padding (A)");
   }
   const std::size_t mp = roundUp(r.m, kern::kHalfGemmBM);
   const std::size_t kp = roundUp(r.k, kern::kHalfGemmBK);
@@ -40,8 +48,16 @@ Status uploadA(HipContext* ctx, MatMulResident& r, const float* a) {
 
 Status uploadB(HipContext* ctx, MatMulResident& r, const float* b) {
   if (!isHalf(r.dtype)) {
-    LC_TRY(r.b.ensure(r.k * r.n * sizeof(float)));
-    return upload(ctx, r.b.get(), b, r.k * r.n * sizeof(float));
+    // fp32: B [roundup(K, 64), roundup(N, 64)], zero pads
+    const std::size_t kp = roundUp(r.k, kern::kF32GemmBK);
+    const std::size_t np = roundUp(r.n, kern::kF32GemmBN);
+    LC_TRY(r.stage.ensure(r.k * r.n * sizeof(float)));
+    LC_TRY(r.b.ensure(kp * np * sizeof(float)));
+    LC_TRY(upload(ctx, r.stage.get(), b, r.k * r.n * sizeof(float)));
+    const hipError_t e = kern::padCopyF32(r.stage.as<float>(), r.b.as<float>(), static_cast<int>(r.k),
+                                          static_cast<int>(r.n), r.n, static_cast<int>(kp), static_cast<int>(np),
+                                          ctx->stream);
+    return e == hipSuccess ? Status::kSuccess : failHip(e, "matmul upload padding (B)");
   }
   const std::size_t np = roundUp(r.n, kern::kHalfGemmBN);
   const std::size_t kp = roundUp(r.k, kern::kHalfGemmBK);
@@ -60,11 +76,12 @@ Status uploadB(HipContext* ctx, MatMulResident& r, const float* b) {
 TuneEntry gemmConfig(const MatMulResident& r) {
   TuneEntry e;
   if (!isHalf(r.dtype)) {
-    e.kernel = "f32_mfma_32x32x2";
-    e.tile_m = 64;
-    e.tile_n = 64;
-    e.tile_k = 16;
-    e.waves = 4;
+    e.kernel = "f32_lds_32x32x2";
+    e.tile_m = kern::kF32GemmBM;
+    e.tile_n = kern::kF32GemmBN;
+    e.tile_k = kern::kF32GemmBK;
+    e.waves = 8;
+    e.split_k = 2;  // two wave groups per block, one per K half of each stage
   } else if (r.m <= 16) {
     e.kernel = "half_skinny_16x16x32";
     e.tile_m = 16;
@@ -98,7 +115,16 @@ hipError_t launchGemm(HipContext* ctx, MatMulResident& r) {
   const int K = static_cast<int>(r.k);
   const int N = static_cast<int>(r.n);
   if (!isHalf(r.dtype)) {
-    return kern::gemmF32(r.a.as<float>(), r.b.as<float>(), r.c.as<float>(), M, N, K, K, N, N, ctx->stream);
+    const int kp = static_cast<int>(roundUp(r.k, kern::kF32GemmBK));
+    const int np = static_cast<int>(roundUp(r.n, kern::kF32GemmBN));
+    // stream-K: one workgroup per CU at most (112 KB of LDS each)
+    const int groups = ctx->props.multiProcessorCount > 0 ? ctx->props.multiProcessorCount : 256;
+    if (ctx->gemm_part.ensure(static_cast<std::size_t>(groups) * 4096 * sizeof(float)) != Status::kSuccess ||
+        ctx->gemm_flags.ensure(static_cast<std::size_t>(groups) * sizeof(int), true) != Status::kSuccess) {
+      return hipErrorOutOfMemory;
+    }
+    return kern::gemmF32Padded(r.a.as<float>(), r.b.as<float>(), r.c.as<float>(), M, N, kp, kp, np, N,
+                               ctx->gemm_part.as<float>(), ctx->gemm_flags.as<int>(), groups, ctx->stream);
   }
   const int kp = static_cast<int>(roundUp(r.k, kern::kHalfGemmBK));
   return kern::gemmHalfTN(r.a.as<uint16_t>(), r.b.as<uint16_t>(), r.c.as<float>(), M, N, kp, kp, kp, N,

@@ -38,8 +38,10 @@ Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnSh
                                 const float* k, const float* v, float* out, const lcAttentionIoPolicy& policy,
                                 std::size_t repeat);
 
-// Device buffers of one GEMM.  fp32: a [M,K], b [K,N]; 16-bit: a [M_pad,K_pad],
-// bt [N_pad,K_pad] (zero padded); c fp32 [M,N]; stage fp32 upload staging.
+// Device buffers of one GEMM, zero padded to the kernel tiles.  fp32:
+// a [roundup(M,64), roundup(K,64)], b [roundup(K,64), roundup(N,64)];
+// 16-bit: a [roundup(M,256), roundup(K,64)], bt [roundup(N,256), roundup(K,64)];
+// c fp32 [M,N]; stage fp32 upload staging.
 struct MatMulResident {
   std::size_t m = 0, k = 0, n = 0;
   lcDataType dtype = LC_DTYPE_F32;

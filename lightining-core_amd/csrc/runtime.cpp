@@ -165,10 +165,11 @@ Status DeviceBuffer::ensure(std::size_t bytes, bool zero) {
   if (bytes <= bytes_ && ptr_ != nullptr) {
     return Status::kSuccess;
   }
+  const std::size_t old = bytes_;
   reset();
   std::size_t want = bytes;
-  if (bytes_ != 0) {
-    want = std::max(bytes, bytes_ + bytes_ / 2);
+  if (old != 0) {
+    want = std::max(bytes, old + old / 2);
   }
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, want);
@@ -184,7 +185,12 @@ Status DeviceBuffer::ensure(std::size_t bytes, bool zero) {
   ptr_ = p;
   bytes_ = want;
   if (zero) {
+    // the null stream does not order with the non-blocking backend stream:
+    // finish the fill before any kernel can read the buffer
     e = hipMemset(ptr_, 0, bytes_);
+    if (e == hipSuccess) {
+      e = hipDeviceSynchronize();
+    }
     if (e != hipSuccess) {
       return failHip(e, "hipMemset");
     }

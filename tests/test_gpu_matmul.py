@@ -48,6 +48,22 @@ def test_matmul_f32_config2(lc, oracle, m, k, n):
     assert_parity(oracle.matmul(a, b), got, "f32", f"f32 {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("m,k,n", [(64, 8192, 64), (512, 4096, 512), (130, 1000, 70), (2048, 96, 2100), (65, 4500, 1)])
+def test_matmul_f32_split_tiles(lc, oracle, m, k, n):
+    # Shapes whose stream-K split puts one tile on several workgroups (up to
+    # 128 partial tiles for 64x8192x64): the sum must match and be the same
+    # bits on every run (partials are added in a fixed order).
+    a = synth.uniform((m, k), stream=13)
+    b = synth.uniform((k, n), stream=14)
+    s = lc.MatMulResidentSession(m, k, n, "f32")
+    s.start_into(a, b)
+    first = s.finish_into().reshape(m, n).copy()
+    s.run_batch_sync_cached_no_download(3)
+    again = s.finish_into().reshape(m, n)
+    assert_parity(oracle.matmul(a, b), first, "f32", f"f32 split {m}x{k}x{n}")
+    np.testing.assert_array_equal(first, again)
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("m,k,n", [(256, 320, 200), (300, 64, 520), (16, 512, 96), (7, 64, 1000), (1, 128, 33)])
 def test_matmul_half_small(lc, oracle, dtype, m, k, n):
