@@ -164,7 +164,7 @@ def bench_config2(lc, synth, steps, warmup, cpu):
     achieved = kflops / (kms * 1e-3) / 1e12
     roofline = {"bound": "mfma", "kernel": "gemm_f32_lds_kernel (1024^3, v_mfma_f32_32x32x2_f32)",
                 "achieved": round(achieved, 3), "peak": PEAK_TFLOPS["f32"], "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_TFLOPS["f32"], 4), "traffic": None,
+                "frac": round(achieved / PEAK_TFLOPS["f32"], 4), "traffic": GEMM_F32_1024_TRAFFIC,
                 "avg_kernel_ms": round(kms, 5), "algorithmic_flops_per_launch": int(kflops)}
 
     cpu_obj = None
@@ -314,12 +314,53 @@ def bench_extras(lc, synth, cpu):
     return out
 
 
+# rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE) over `bench.py
+# --pmc-workload`: the copy kernel behind a device-to-device lcMemcpy moves a
+# known number of bytes each way, which calibrates each counter; the GEMM's
+# per-dispatch means times those factors give its HBM traffic.  Figures from
+# profiles/gemm_f32_lds_kernel_1024_traffic.txt (update them when the kernel
+# changes).
+PMC_COPY_BYTES = 256 << 20
+PMC_COPIES = 10
+PMC_GEMMS = 20
+# FETCH_SIZE: GEMM 12338.3 KiB/dispatch, copy 131084.4 KiB for 262144 KiB moved (x2.000);
+# WRITE_SIZE: GEMM 4096.0 KiB/dispatch, copy 262144.0 KiB (x1.000).
+GEMM_F32_1024_TRAFFIC = 25266448 + 4194304  # HBM bytes per launch (fetch + write, calibrated)
+
+
+def pmc_workload(lc, synth):
+    lib = lc._core._lib()
+    src, dst = ctypes.c_void_p(), ctypes.c_void_p()
+    if lib.lcMalloc(ctypes.byref(src), PMC_COPY_BYTES) != 0 or lib.lcMalloc(ctypes.byref(dst), PMC_COPY_BYTES) != 0:
+        raise RuntimeError("lcMalloc failed")
+    try:
+        for _ in range(PMC_COPIES):
+            if lib.lcMemcpy(dst, src, PMC_COPY_BYTES, 3) != 0:  # LC_MEMCPY_DEVICE_TO_DEVICE
+                raise RuntimeError("lcMemcpy failed")
+        lc.device_synchronize()
+    finally:
+        lib.lcFree(src)
+        lib.lcFree(dst)
+    a = synth.uniform((1024, 1024), stream=100)
+    b = synth.uniform((1024, 1024), stream=101)
+    s = lc.MatMulResidentSession(1024, 1024, 1024, "f32")
+    s.start_into(a, b)
+    s.run_batch_sync_cached_no_download(PMC_GEMMS)
+    lc.device_synchronize()
+    s.close()
+    log(f"[bench] pmc workload done: {PMC_COPIES} copies of {PMC_COPY_BYTES} bytes, {PMC_GEMMS} GEMM launches")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--pmc-workload", action="store_true",
+                    help="run only the fixed workload the rocprofv3 --pmc traffic passes count: "
+                         f"{PMC_COPIES} device-to-device copies of {PMC_COPY_BYTES >> 20} MiB (calibration) "
+                         f"and {PMC_GEMMS} launches of the 1024^3 fp32 GEMM")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py: this build measures one GPU only (the path is single-GPU; see DESIGN.md for how it would "
@@ -334,6 +375,9 @@ def main():
         sys.exit(1)
     info = lc.device_info()
     log(f"[bench] device {info}")
+    if args.pmc_workload:
+        pmc_workload(lc, synth)
+        return
     cpu = CpuBaseline()
     value, ms_per_step, roofline, cpu_obj = bench_config2(lc, synth, args.steps, args.warmup, cpu)
     log(f"[bench] config2: {value:.3f} TFLOP/s, {ms_per_step:.4f} ms/step, kernel {roofline}")
