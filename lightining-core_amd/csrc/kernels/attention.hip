@@ -149,10 +149,23 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restric
 }
 
 // ---------------------------------------------------------------------------
-// 16-bit: 4 waves x 32 queries per workgroup, 64-key tiles.  K tile and V^T
-// tile are double-buffered in LDS; the next tile is prefetched into registers
-// while the current one is computed, so each tile costs one barrier.  Q
-// fragments live in registers; v_mfma_f32_32x32x16_{bf16,f16}.
+// 16-bit: 4 waves x 32 queries per workgroup, 64-key tiles, software
+// pipelined.  While a wave turns tile j's scores into probabilities (VALU),
+// the MFMAs of tile j+1's scores are already in flight; then tile j's P.V
+// MFMAs.  K and V^T tiles reach LDS by direct global -> LDS loads (no staging
+// registers, no LDS store instructions), two buffers each: K of tile j+2 and
+// V^T of tile j+1 load while tile j is processed; one wait + barrier per tile.
+// Q fragments live in registers; v_mfma_f32_32x32x16_{bf16,f16}.
+//
+// LDS layouts, 16-byte chunks XOR-swizzled so that every fragment read is
+// conflict-free (a 16-byte read serves 16 lanes per clock over 64 banks):
+//   K tile   [64 keys][D]  rows of 2D bytes: chunk ^ (row & 15) for 256-byte
+//                          rows, chunk ^ ((row >> 1) & 7) for 128-byte rows
+//   V^T tile [D][64 keys]  128-byte rows: chunk ^ ((row >> 1) & 7)
+// Key order: MFMA row m of a 32-key block reads key pi(m), pi swapping bits 2
+// and 3 of m.  Accumulator register i of lane l then holds key
+// 16*(i/8) + 8*(l/32) + i%8, so the 8 probabilities a lane feeds to one P.V
+// MFMA are 8 consecutive keys and its V^T operand is one 16-byte read.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -163,14 +176,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
                                                                uint16_t* __restrict__ Ocat, int heads, int S,
                                                                int S_pad, int causal, float scale) {
   constexpr int KT = 64;
-  constexpr int LDK = D + 8;
-  constexpr int LDV = KT + 8;
+  constexpr int KCH = D / 8;               // 16-byte chunks per K row
+  constexpr int K_RPI = 64 / KCH;          // K rows per 1 KB load instruction
+  constexpr int TILE = KT * D;             // elements of a K (or V^T) tile
+  constexpr int LPW = TILE * 2 / 1024 / 4; // load instructions per wave per operand
   constexpr int DT = D / 32;
   constexpr int QS = D / 16;
-  constexpr int KCH = KT * D / 8 / 256;  // 16-byte chunks of the K tile per thread
-  constexpr int VCH = D * KT / 8 / 256;  // ... of the V^T tile
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][KT * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][D * LDV];
+  static_assert(D == 64 || D == 128, "head dim");
+  // One LDS array: K buffers at 0 and TILE, V^T buffers at 2*TILE and
+  // 3*TILE.  (With separate __shared__ arrays the compiler puts a full
+  // vmcnt(0) in front of the first LDS read after every global -> LDS load,
+  // which would expose the load latency of each tile.)
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -181,43 +198,40 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   const int q0 = qb * 128 + wave * 32;
   const size_t hoff = static_cast<size_t>(bh) * S_pad * D;
   const uint16_t* Qh = Q + hoff;
-  const uint16_t* Kh = K + hoff;
-  const uint16_t* Vh = Vt + hoff;
   const int lrow = lane & 31;
   const int half = lane >> 5;
 
-  u32x4 kreg[KCH];
-  u32x4 vreg[VCH];
-  auto load_tile = [&](int j0) {
+  // Load mapping: wave w issues instructions w + 4j (j < LPW) of each operand.
+  // K instruction i fills rows K_RPI*i + lane / KCH, physical chunk lane % KCH;
+  // V^T instruction i fills rows 8i + lane / 8, physical chunk lane % 8.
+  // Per-lane element offsets are 32-bit (a head is far below 2^31
+  // elements); the tile base is uniform, so the loads take the
+  // scalar-base + vector-offset form and the offsets cost one VGPR each.
+  const uint16_t* Kh = K + hoff;
+  const uint16_t* Vh = Vt + hoff;
+  int k_off[LPW];
+  int v_off[LPW];
 #pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int ch = c * 256 + tid;
-      const int r = ch / (D / 8);
-      const int col = (ch - r * (D / 8)) * 8;
-      kreg[c] = *reinterpret_cast<const u32x4*>(Kh + static_cast<size_t>(j0 + r) * D + col);
-    }
+  for (int j = 0; j < LPW; ++j) {
+    const int ins = wave + 4 * j;
+    const int kr = K_RPI * ins + lane / KCH;
+    const int kswz = KCH == 16 ? (kr & 15) : ((kr >> 1) & 7);
+    k_off[j] = kr * D + ((lane % KCH) ^ kswz) * 8;
+    const int vr = 8 * ins + (lane >> 3);
+    v_off[j] = vr * S_pad + ((lane & 7) ^ ((vr >> 1) & 7)) * 8;
+  }
+  auto issue_k = [&](int buf, int tile) {
+    const uint16_t* base = Kh + static_cast<size_t>(tile) * KT * D;
 #pragma unroll
-    for (int c = 0; c < VCH; ++c) {
-      const int ch = c * 256 + tid;
-      const int r = ch / (KT / 8);
-      const int col = (ch - r * (KT / 8)) * 8;
-      vreg[c] = *reinterpret_cast<const u32x4*>(Vh + static_cast<size_t>(r) * S_pad + j0 + col);
+    for (int j = 0; j < LPW; ++j) {
+      load_lds16(base + k_off[j], smem + buf * TILE + (wave + 4 * j) * 512);
     }
   };
-  auto store_tile = [&](int buf) {
+  auto issue_v = [&](int buf, int tile) {
+    const uint16_t* base = Vh + tile * KT;
 #pragma unroll
-    for (int c = 0; c < KCH; ++c) {
-      const int ch = c * 256 + tid;
-      const int r = ch / (D / 8);
-      const int col = (ch - r * (D / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&Ks[buf][r * LDK + col]) = kreg[c];
-    }
-#pragma unroll
-    for (int c = 0; c < VCH; ++c) {
-      const int ch = c * 256 + tid;
-      const int r = ch / (KT / 8);
-      const int col = (ch - r * (KT / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&Vs[buf][r * LDV + col]) = vreg[c];
+    for (int j = 0; j < LPW; ++j) {
+      load_lds16(base + v_off[j], smem + (2 + buf) * TILE + (wave + 4 * j) * 512);
     }
   };
 
@@ -226,6 +240,25 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   for (int s = 0; s < QS; ++s) {
     qf[s] = *reinterpret_cast<const u32x4*>(Qh + static_cast<size_t>(q0 + lrow) * D + s * 16 + 8 * half);
   }
+
+  // Fragment addresses (elements).  K: MFMA row lrow of 32-key block kt reads
+  // key kt*32 + pi(lrow); its swizzle does not depend on kt.
+  const int prow = (lrow & ~12) | ((lrow & 4) << 1) | ((lrow & 8) >> 1);
+  const int kswz = KCH == 16 ? (prow & 15) : ((prow >> 1) & 7);
+  const int vswz = (lrow >> 1) & 7;
+  auto qk = [&](const uint16_t* ks, floatx16 (&sc)[2]) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      sc[kt] = zero16();
+#pragma unroll
+      for (int s = 0; s < QS; ++s) {
+        const u32x4 a =
+            *reinterpret_cast<const u32x4*>(ks + (kt * 32 + prow) * D + (((2 * s + half) ^ kswz) << 3));
+        sc[kt] = mfma32x32x16<T>(a, qf[s], sc[kt]);
+      }
+    }
+  };
+
   floatx16 o[DT];
 #pragma unroll
   for (int t = 0; t < DT; ++t) {
@@ -236,107 +269,158 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   const int qi = q0 + lrow;
   const float c = scale * kLog2e;
   const int kend = causal ? min(S, qb * 128 + 128) : S;
+  const int nt = (kend + KT - 1) / KT;
+  // Causal: tile j is skipped by a wave whose queries all precede its keys
+  // (monotone in j: a skipped tile is followed only by skipped tiles).
+  auto active = [&](int j) { return !(causal && j * KT > q0 + 31); };
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  int buf = 0;
-  for (int j0 = 0; j0 < kend; j0 += KT) {
-    const bool more = j0 + KT < kend;
-    if (more) {
-      load_tile(j0 + KT);
-    }
-    if (!(causal && j0 > q0 + 31)) {  // else every key of the tile follows every query of this wave
-      const uint16_t* ks = Ks[buf];
-      const uint16_t* vs = Vs[buf];
-      floatx16 sc[2];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        sc[kt] = zero16();
-#pragma unroll
-        for (int s = 0; s < QS; ++s) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(&ks[(kt * 32 + lrow) * LDK + s * 16 + 8 * half]);
-          sc[kt] = mfma32x32x16<T>(a, qf[s], sc[kt]);
-        }
-      }
-      // Raw scores s = q.k; the scale is applied inside the exponent:
-      // p = exp2(s*c - m*c) with m the running max of raw scores (c > 0).
-      const bool need_mask = (j0 + KT > S) || (causal && j0 + KT - 1 > q0);
-      if (need_mask) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int key = j0 + kt * 32 + acc_row(i, lane);
-            if (key >= S || (causal && key > qi)) {
-              sc[kt][i] = kMaskValue;
-            }
-          }
-        }
-      }
-      float mt = kMaskValue;
+  // Tile j's probabilities from its raw scores sc (p = exp2(s*c - m*c), m the
+  // running max of raw scores), optionally with tile j+1's QK^T MFMAs in the
+  // same basic block (so the scheduler interleaves them with the VALU work),
+  // then tile j's O^T += V^T . P^T.
+  floatx16 s_a[2];
+  floatx16 s_b[2];
+  auto step = [&](int j, floatx16 (&s_cur)[2], floatx16 (&s_nxt)[2]) {
+    const int j0 = j * KT;
+    if ((j0 + KT > S) || (causal && j0 + KT - 1 > q0)) {
+      // key = j0 + 8*half + off with off a compile-time constant per register;
+      // masked when key >= S or (causal) key > qi, i.e. off > lim.
+      const int lim = (causal ? min(qi, S - 1) : S - 1) - j0 - 8 * half;
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          mt = fmaxf(mt, sc[kt][i]);
-        }
-      }
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      // Rescale O and l only when some lane's max grew by more than 8/c
-      // (exp2 units); otherwise keep the stale reference max.  O and l always
-      // share the same reference, so O/l is unchanged; exponents stay <= 8.
-      const float m_cand = fmaxf(m_run, mt);
-      if (__any((m_cand - m_run) * c > 8.0f)) {
-        const float alpha = fast_exp2((m_run - m_cand) * c);
-        m_run = m_cand;
-        l_run *= alpha;
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            o[t][i] *= alpha;
+          if (kt * 32 + 16 * (i >> 3) + (i & 7) > lim) {
+            s_cur[kt][i] = kMaskValue;
           }
         }
       }
-      const float mc = m_run * c;
-      float ls = 0.0f;
+    }
+    float mt = kMaskValue;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        mt = fmaxf(mt, s_cur[kt][i]);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    // Rescale O and l only when some lane's max grew by more than 8 (exp2
+    // units); otherwise keep the stale reference max.  O and l always share
+    // the same reference, so O/l is unchanged; exponents stay <= 8.
+    const float m_cand = fmaxf(m_run, mt);
+    if (__any((m_cand - m_run) * c > 8.0f)) {
+      const float alpha = fast_exp2((m_run - m_cand) * c);
+      m_run = m_cand;
+      l_run *= alpha;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float p = fast_exp2(__builtin_fmaf(sc[kt][i], c, -mc));
-          sc[kt][i] = p;
-          ls += p;
-        }
-      }
-      l_run += ls;
-      // O^T += V^T . P^T over 4 key-steps of 16; element j of step ks is key
-      // 16*ks + 8*(j/4) + 4*half + j%4 = accumulator register 8*(ks&1) + j of sc[ks>>1].
-#pragma unroll
-      for (int ks2 = 0; ks2 < 4; ++ks2) {
-        const floatx16& p = sc[ks2 >> 1];
-        const int b0 = (ks2 & 1) * 8;
-        u32x4 pb;
-        pb[0] = pack2<T>(p[b0 + 0], p[b0 + 1]);
-        pb[1] = pack2<T>(p[b0 + 2], p[b0 + 3]);
-        pb[2] = pack2<T>(p[b0 + 4], p[b0 + 5]);
-        pb[3] = pack2<T>(p[b0 + 6], p[b0 + 7]);
-#pragma unroll
-        for (int t = 0; t < DT; ++t) {
-          const uint16_t* vp = &vs[(t * 32 + lrow) * LDV + 16 * ks2 + 4 * half];
-          const u32x2 lo = *reinterpret_cast<const u32x2*>(vp);
-          const u32x2 hi = *reinterpret_cast<const u32x2*>(vp + 8);
-          const u32x4 va{lo[0], lo[1], hi[0], hi[1]};
-          o[t] = mfma32x32x16<T>(va, pb, o[t]);
+          o[t][i] *= alpha;
         }
       }
     }
-    if (more) {
-      store_tile(buf ^ 1);
+    // Phase 1: the 32 exponentials of this lane, packed to 16-bit pairs as
+    // they come, with the next tile's 2*QS QK^T MFMAs issued between them
+    // (EPM exponentials per MFMA, K fragments read two MFMAs ahead).  The
+    // sched_barrier after each group keeps this order: an MFMA runs for 32
+    // clocks while the wave issues the group's VALU work behind it.
+    constexpr int NQK = 2 * QS;
+    constexpr int EPM = 32 / NQK;
+    const float mc = m_run * c;
+    float ls = 0.0f;
+    u32x4 pb[4];
+    const uint16_t* ksn = smem + ((j + 1) & 1) * TILE;
+    auto kfrag = [&](int g) {
+      const int kt = g / QS;
+      const int s = g - kt * QS;
+      return *reinterpret_cast<const u32x4*>(ksn + (kt * 32 + prow) * D + (((2 * s + half) ^ kswz) << 3));
+    };
+    u32x4 kf0 = kfrag(0);
+    u32x4 kf1 = kfrag(1);
+#pragma unroll
+    for (int g = 0; g < NQK; ++g) {
+      u32x4 kf2;
+      if (g + 2 < NQK) {
+        kf2 = kfrag(g + 2);
+      }
+      {
+        const int kt = g / QS;
+        const int s = g - kt * QS;
+        s_nxt[kt] = mfma32x32x16<T>(kf0, qf[s], s == 0 ? zero16() : s_nxt[kt]);
+      }
+#pragma unroll
+      for (int e = 0; e < EPM; e += 2) {
+        const int idx = g * EPM + e;  // score element idx and idx + 1
+        const float p0 = fast_exp2(__builtin_fmaf(s_cur[idx >> 4][idx & 15], c, -mc));
+        const float p1 = fast_exp2(__builtin_fmaf(s_cur[idx >> 4][(idx & 15) + 1], c, -mc));
+        ls += p0 + p1;
+        pb[idx >> 3][(idx & 7) >> 1] = pack2<T>(p0, p1);
+      }
+      kf0 = kf1;
+      kf1 = kf2;
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
-    buf ^= 1;
+    l_run += ls;
+    // Phase 2: O^T += V^T . P^T, V^T fragments read two MFMAs ahead.
+    const uint16_t* vs = smem + (2 + (j & 1)) * TILE;
+    auto vfrag = [&](int g) {
+      const int ks2 = g / DT;
+      const int t = g - ks2 * DT;
+      return *reinterpret_cast<const u32x4*>(vs + (t * 32 + lrow) * KT + (((2 * ks2 + half) ^ vswz) << 3));
+    };
+    constexpr int NPV = 4 * DT;
+    u32x4 vf0 = vfrag(0);
+    u32x4 vf1 = vfrag(1);
+#pragma unroll
+    for (int g = 0; g < NPV; ++g) {
+      u32x4 vf2;
+      if (g + 2 < NPV) {
+        vf2 = vfrag(g + 2);
+      }
+      const int ks2 = g / DT;
+      const int t = g - ks2 * DT;
+      o[t] = mfma32x32x16<T>(vf0, pb[ks2], o[t]);
+      vf0 = vf1;
+      vf1 = vf2;
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  issue_k(0, 0);
+  issue_v(0, 0);
+  if (nt > 1) {
+    issue_k(1, 1);
+  }
+  wait_vmcnt<0>();
+  stage_barrier();
+  qk(smem, s_a);     // tile 0 is active for every wave
+  stage_barrier();   // K buffer 0 is refilled next
+  // One tile: its loads of K(j+2) and V^T(j+1) go out first, then the
+  // pipelined step (the next tile's scores are computed unconditionally, one
+  // code path; past the last tile, or when the next tile is skipped, they
+  // come from a stale but stable K buffer and go unused), then the wait and
+  // barrier.  Unrolled by two so the score registers swap roles instead of
+  // being copied.
+  auto tile = [&](int j, floatx16 (&s_cur)[2], floatx16 (&s_nxt)[2]) {
+    if (j + 2 < nt) {
+      issue_k(j & 1, j + 2);
+    }
+    if (j + 1 < nt) {
+      issue_v((j + 1) & 1, j + 1);
+    }
+    if (active(j)) {
+      step(j, s_cur, s_nxt);
+    }
+    wait_vmcnt<0>();  // this wave's loads of K(j+2) and V^T(j+1) have landed
+    stage_barrier();  // everyone's have; everyone is done with K(j+1) and V^T(j)
+  };
+  for (int j = 0; j < nt; j += 2) {
+    tile(j, s_a, s_b);
+    if (j + 1 < nt) {
+      tile(j + 1, s_b, s_a);
+    }
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);

@@ -536,38 +536,6 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(const uint16_t*
 
 constexpr int kHBK = 64;
 
-// 16-byte global -> LDS copy of one lane (LDS address = lds_base + 16*lane).
-// A plain (non-template) device function: used directly inside a kernel
-// template whose body depends on template parameters, the target builtin
-// makes the host-side instantiation fail silently and no launch stub is
-// emitted.
-__device__ __forceinline__ void load_lds16(const uint16_t* src, uint16_t* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
-}
-__device__ __forceinline__ void load_lds16(const float* src, float* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(n) for the small n the pipelines use (expcnt / lgkmcnt
-// left at their maxima; vmcnt's low four bits sit in bits 3:0).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | N);
-}
-
-// Workgroup barrier without the release fence of __syncthreads(): the fence
-// would make the compiler drain every outstanding global -> LDS load
-// (vmcnt(0)) at each stage and collapse a multi-stage pipeline.  Callers wait
-// for exactly the stage they need with s_waitcnt vmcnt(n) first; every LDS
-// read of the retiring stage has already been consumed by its MFMA.  The empty
-// asm statements keep the compiler from moving memory operations across.
-__device__ __forceinline__ void stage_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // ---------------------------------------------------------------------------
 // Large-tile 16-bit TN GEMM with direct global -> LDS loads.
 //
