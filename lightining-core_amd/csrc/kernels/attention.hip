@@ -26,19 +26,27 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kMaskValue = -1e30f;
 
 // ---------------------------------------------------------------------------
-// fp32: one wave per 32 queries, 32-key tiles in LDS, v_mfma_f32_32x32x2_f32.
-// D padded to 32*DT (zeros).
+// fp32: KS waves per 32 queries, v_mfma_f32_32x32x2_f32, D padded to 32*DT
+// (zeros).  Wave w of the workgroup takes the 32-key tiles j = w, w+KS, ...
+// with its own K / V tiles in LDS and its own online-softmax state; the KS
+// partial states are merged through LDS at the end (m = max m_w, O and l
+// rescaled by exp2(m_w - m) and summed in wave order).  KS > 1 puts more
+// waves on small problems (one head of S = 256 is 8 query blocks).
 // ---------------------------------------------------------------------------
-template <int DT>
-__global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                          const float* __restrict__ v, float* __restrict__ out,
-                                                          int S, int D, int causal, float scale, float post_scale,
-                                                          float post_bias, int post_relu) {
+template <int DT, int KS, bool VEC>
+__global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __restrict__ q,
+                                                               const float* __restrict__ k,
+                                                               const float* __restrict__ v, float* __restrict__ out,
+                                                               int S, int D, int causal, float scale,
+                                                               float post_scale, float post_bias, int post_relu) {
   constexpr int DP = 32 * DT;
+  constexpr int KV = 32 * (DP + 1) + 32 * DP;  // floats of one wave's K + V tile
   __shared__ float Qs[32][DP + 1];
-  __shared__ float Ks[32][DP + 1];
-  __shared__ float Vs[32][DP];
-  const int lane = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) float kv[KS][KV];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float (*Ks)[DP + 1] = reinterpret_cast<float (*)[DP + 1]>(&kv[wave][0]);
+  float (*Vs)[DP] = reinterpret_cast<float (*)[DP]>(&kv[wave][32 * (DP + 1)]);
   const int nqb = (S + 31) / 32;
   const int qb = nqb - 1 - static_cast<int>(blockIdx.x);  // heaviest (causal) blocks first
   const int q0 = qb * 32;
@@ -48,12 +56,12 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restric
   v += head;
   out += head;
 
-  for (int idx = lane; idx < 32 * DP; idx += 64) {
+  for (int idx = threadIdx.x; idx < 32 * DP; idx += 64 * KS) {
     const int r = idx / DP;
     const int c = idx - r * DP;
     Qs[r][c] = (q0 + r < S && c < D) ? q[static_cast<size_t>(q0 + r) * D + c] : 0.0f;
   }
-  const int dsteps = (D + 1) / 2 * 2;  // k-extent of S^T = K . Q^T (zero padded)
+  __syncthreads();
 
   floatx16 o[DT];
 #pragma unroll
@@ -65,19 +73,62 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restric
   const int qi = q0 + (lane & 31);
   const int kend = causal ? min(S, q0 + 32) : S;
 
-  for (int j0 = 0; j0 < kend; j0 += 32) {
-    __syncthreads();
-    for (int idx = lane; idx < 32 * DP; idx += 64) {
-      const int r = idx / DP;
-      const int cc = idx - r * DP;
-      const bool ok = (j0 + r < S && cc < D);
-      Ks[r][cc] = ok ? k[static_cast<size_t>(j0 + r) * D + cc] : 0.0f;
-      Vs[r][cc] = ok ? v[static_cast<size_t>(j0 + r) * D + cc] : 0.0f;
+  // Only this wave touches its K / V tiles: wave-level ordering suffices
+  // (LDS accesses of one wave complete in order).  VEC (D % 4 == 0, 16-byte
+  // aligned rows, DT <= 2): each lane holds CH float4 of the next tile's K
+  // and V in registers, loaded while the current tile is computed.
+  constexpr int CH = DP / 8;  // float4 chunks per lane per operand
+  float4 kr[VEC ? CH : 1];
+  float4 vr[VEC ? CH : 1];
+  auto fetch = [&](int j0) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int idx = c * 64 + lane;  // chunk: row idx / (DP/4), column 4 * (idx % (DP/4))
+      const int r = idx / (DP / 4);
+      const int cc = (idx - r * (DP / 4)) * 4;
+      const bool ok = j0 + r < S && cc < D;
+      const size_t off = static_cast<size_t>(j0 + r) * D + cc;
+      kr[c] = ok ? *reinterpret_cast<const float4*>(k + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      vr[c] = ok ? *reinterpret_cast<const float4*>(v + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    __syncthreads();
+  };
+  if constexpr (VEC) {
+    if (wave * 32 < kend) {
+      fetch(wave * 32);
+    }
+  }
+  for (int j0 = wave * 32; j0 < kend; j0 += 32 * KS) {
+    if constexpr (VEC) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int idx = c * 64 + lane;
+        const int r = idx / (DP / 4);
+        const int cc = (idx - r * (DP / 4)) * 4;
+        Ks[r][cc] = kr[c].x;
+        Ks[r][cc + 1] = kr[c].y;
+        Ks[r][cc + 2] = kr[c].z;
+        Ks[r][cc + 3] = kr[c].w;
+        *reinterpret_cast<float4*>(&Vs[r][cc]) = vr[c];
+      }
+      if (j0 + 32 * KS < kend) {
+        fetch(j0 + 32 * KS);
+      }
+    } else {
+      for (int idx = lane; idx < 32 * DP; idx += 64) {
+        const int r = idx / DP;
+        const int cc = idx - r * DP;
+        const bool ok = (j0 + r < S && cc < D);
+        Ks[r][cc] = ok ? k[static_cast<size_t>(j0 + r) * D + cc] : 0.0f;
+        Vs[r][cc] = ok ? v[static_cast<size_t>(j0 + r) * D + cc] : 0.0f;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
 
+    // Over the padded DP (columns D..DP-1 of both tiles are zero): a
+    // compile-time trip count lets the LDS reads run ahead of the MFMAs.
     floatx16 st = zero16();
-    for (int dd = 0; dd < dsteps; dd += 2) {
+#pragma unroll
+    for (int dd = 0; dd < DP; dd += 2) {
       const float a = Ks[lane & 31][dd + (lane >> 5)];
       const float b = Qs[lane & 31][dd + (lane >> 5)];
       st = mfma32x32x2f32(a, b, st);
@@ -123,10 +174,58 @@ __global__ __launch_bounds__(64) void attn_fwd_f32_kernel(const float* __restric
         o[t] = mfma32x32x2f32(a, st[s], o[t]);
       }
     }
+    __builtin_amdgcn_wave_barrier();  // the next tile overwrites K / V of this one
   }
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = 1.0f / l_tot;
+  l_run += __shfl_xor(l_run, 32);
+  float inv = 1.0f / l_run;
+  if constexpr (KS > 1) {
+    // Park each wave's state in its own K / V region: m, l (32 each), then
+    // O^T as [d][query].  A wave that saw no key tile parks m = -1e30, l = 0.
+    float* mine = &kv[wave][0];
+    if (lane < 32) {
+      mine[lane] = m_run;
+      mine[32 + lane] = l_run;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        mine[64 + (t * 32 + acc_row(i, lane)) * 32 + (lane & 31)] = o[t][i];
+      }
+    }
+    __syncthreads();
+    if (wave != 0) {
+      return;
+    }
+    const int ql = lane & 31;
+    float m_all = kMaskValue;
+#pragma unroll
+    for (int w = 0; w < KS; ++w) {
+      m_all = fmaxf(m_all, kv[w][ql]);
+    }
+    float f[KS];
+    float l_all = 0.0f;
+#pragma unroll
+    for (int w = 0; w < KS; ++w) {
+      f[w] = exp2f(kv[w][ql] - m_all);
+      l_all += f[w] * kv[w][32 + ql];
+    }
+    inv = 1.0f / l_all;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int d = t * 32 + acc_row(i, lane);
+        float acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KS; ++w) {
+          acc += f[w] * kv[w][64 + d * 32 + ql];
+        }
+        o[t][i] = acc;
+      }
+    }
+  }
   if (qi < S) {
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
@@ -469,22 +568,47 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
     return hipErrorInvalidValue;
   }
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
-  const dim3 grid((S + 31) / 32, bh);
+  const int nqb = (S + 31) / 32;
+  const dim3 grid(nqb, bh);
   const int dt = (D + 31) / 32;
   const int cz = causal ? 1 : 0;
-#define LC_ATTN_F32(DT_)                                                                                            \
-  hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_>), grid, dim3(64), 0, stream, q, k, v, out, S, D, cz, scale,           \
-                     post_scale, post_bias, post_relu)
-  switch (dt) {
-    case 1: LC_ATTN_F32(1); break;
-    case 2: LC_ATTN_F32(2); break;
-    case 3: LC_ATTN_F32(3); break;
-    case 4: LC_ATTN_F32(4); break;
-    case 5: LC_ATTN_F32(5); break;
-    case 6: LC_ATTN_F32(6); break;
-    case 7: LC_ATTN_F32(7); break;
-    default: LC_ATTN_F32(8); break;
+  // Key splits: enough waves for about two per CU, at most one split per
+  // 32-key tile, and K + V tiles of every wave within the 160 KB of LDS
+  // (8 splits at DT = 2: 140 KB).
+  const int tiles = nqb;
+  int ks = 1;
+  while (ks < 8 && static_cast<long long>(nqb) * bh * ks * 2 <= 512 && ks * 2 <= tiles &&
+         (ks * 2) * dt <= (dt <= 2 ? 16 : 8)) {
+    ks *= 2;
   }
+  const bool vec = dt <= 2 && D % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                   reinterpret_cast<uintptr_t>(v) % 16 == 0;
+#define LC_ATTN_F32(DT_, KS_)                                                                                       \
+  if (vec && (DT_) <= 2) {                                                                                          \
+    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, ((DT_) <= 2)>), grid, dim3(64 * (KS_)), 0, stream, q, k, v,   \
+                       out, S, D, cz, scale, post_scale, post_bias, post_relu);                                     \
+  } else {                                                                                                          \
+    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out, S,  \
+                       D, cz, scale, post_scale, post_bias, post_relu);                                             \
+  }
+#define LC_ATTN_F32_KS(DT_)                                                                                         \
+  switch (ks) {                                                                                                     \
+    case 8: LC_ATTN_F32(DT_, (DT_ <= 2 ? 8 : 1)); break;                                                            \
+    case 4: LC_ATTN_F32(DT_, (DT_ <= 2 ? 4 : 1)); break;                                                            \
+    case 2: LC_ATTN_F32(DT_, (DT_ <= 4 ? 2 : 1)); break;                                                            \
+    default: LC_ATTN_F32(DT_, 1); break;                                                                            \
+  }
+  switch (dt) {
+    case 1: LC_ATTN_F32_KS(1); break;
+    case 2: LC_ATTN_F32_KS(2); break;
+    case 3: LC_ATTN_F32_KS(3); break;
+    case 4: LC_ATTN_F32_KS(4); break;
+    case 5: LC_ATTN_F32(5, 1); break;
+    case 6: LC_ATTN_F32(6, 1); break;
+    case 7: LC_ATTN_F32(7, 1); break;
+    default: LC_ATTN_F32(8, 1); break;
+  }
+#undef LC_ATTN_F32_KS
 #undef LC_ATTN_F32
   return hipGetLastError();
 }
