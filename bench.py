@@ -244,7 +244,7 @@ def bench_extras(lc, synth, cpu):
     cpu_tf = sample = None
     if cpu.orc is not None:
         qr, kr, vr = (synth.round_bf16(x[0, 0]) for x in (q, k, v))
-        rows = 32
+        rows = 256
         t0 = time.perf_counter()
         for r in np.linspace(0, s - 1, rows).astype(int):
             cpu.attention_rows(qr, kr, vr, True, int(r), int(r) + 1)
