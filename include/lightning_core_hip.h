@@ -285,6 +285,33 @@ lcError_t lcAttentionSessionForwardWithPolicy(lcAttentionSession* session, const
  * MatMulMetalResidentSession::runBatchSyncCachedNoDownload (ops.hpp:1371-1373). */
 lcError_t lcAttentionSessionRunCached(lcAttentionSession* session, size_t repeat_count);
 
+/* Attention train step, fp32, one head [S, D] (the reference's dV-only SGD
+ * step): out = attention(q, k, v) (no postprocess), loss = mean((out -
+ * target)^2), v -= learning_rate * P^T . 2 (out - target) / (S*D).  v is
+ * in/out: with download_v the updated V is copied back into it.  Null
+ * pointers, zero dims or learning_rate <= 0 -> LC_INVALID_VALUE regardless of
+ * the policy (src/attention.cpp:229-232).  loss_out may be NULL (no loss).
+ * attentionTrainStep (src/attention.cpp:203-214). */
+lcError_t lcAttentionTrainStep(const float* q, const float* k, float* v, const float* target, float* out,
+                               float learning_rate, const lcAttentionConfig* cfg, lcDeviceKind device,
+                               float* loss_out);
+/* attentionTrainStepWithPolicy (src/attention.cpp:217-244): upload_q/k/v/
+ * target = 0 reuse the backend-global resident tensors, download_out /
+ * download_v / synchronize as for the forward. */
+lcError_t lcAttentionTrainStepWithPolicy(const float* q, const float* k, float* v, const float* target, float* out,
+                                         float learning_rate, const lcAttentionConfig* cfg, lcDeviceKind device,
+                                         float* loss_out, const lcAttentionIoPolicy* policy);
+/* AttentionSession::trainStep / trainStepWithPolicy (src/attention.cpp:
+ * 285-343): on the session's own resident tensors; with loss_out, the loss is
+ * measured every loss_every steps (0 = shape-aware default, :12-39) and the
+ * last measured value is returned in between, when a step downloads nothing
+ * it then does not block. */
+lcError_t lcAttentionSessionTrainStep(lcAttentionSession* session, const float* q, const float* k, float* v,
+                                      const float* target, float* out, float learning_rate, float* loss_out);
+lcError_t lcAttentionSessionTrainStepWithPolicy(lcAttentionSession* session, const float* q, const float* k,
+                                                float* v, const float* target, float* out, float learning_rate,
+                                                float* loss_out, const lcAttentionIoPolicy* policy);
+
 /* --- matmul ------------------------------------------------------------------ */
 
 /* MatMulIoPolicy (reference include/lightning_core/core/ops/policy.hpp:8-13). */

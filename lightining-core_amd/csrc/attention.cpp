@@ -129,7 +129,8 @@ Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnSh
     hipError_t e;
     if (!half) {
       e = kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(), bh, S, D,
-                             sh.causal, policy.output_scale, policy.output_bias, policy.output_relu, ctx->stream);
+                             sh.causal, policy.output_scale, policy.output_bias, policy.output_relu, nullptr,
+                             ctx->stream);
     } else {
       e = kern::attentionHalf(res.q.as<uint16_t>(), res.k.as<uint16_t>(), res.v.as<uint16_t>(), res.out.as<float>(),
                               nullptr, static_cast<int>(sh.heads), bh, S, static_cast<int>(sh.sPad()), D, sh.causal,
@@ -148,6 +149,88 @@ Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnSh
     LC_TRY(download(ctx, out, res.out.get(), n * sizeof(float)));
   }
   if (policy.download_out || policy.synchronize) {
+    LC_TRY(syncStream(ctx));
+  }
+  return Status::kSuccess;
+}
+
+Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShape& sh, const float* q,
+                              const float* k, float* v, const float* target, float* out, float learning_rate,
+                              float* loss_out, const lcAttentionIoPolicy& policy) {
+  // src/attention.cpp:229-232: every pointer, both dims and a positive
+  // learning rate are required, whatever the policy.
+  if (q == nullptr || k == nullptr || v == nullptr || target == nullptr || out == nullptr || sh.seq_len == 0 ||
+      sh.head_dim == 0 || !(learning_rate > 0.0f)) {
+    return fail(Status::kInvalidValue, "attention train step: null pointer, zero dimension or learning_rate <= 0");
+  }
+  if (isHalf(sh.dtype) || sh.bh() != 1) {
+    return fail(Status::kNotSupported, "attention train step: fp32, one head (the reference's [S, D] step)");
+  }
+  if (sh.head_dim > 256 || sh.seq_len > (1u << 24)) {
+    return fail(Status::kNotSupported, "attention train step: head_dim <= 256");
+  }
+  if (!sameShape(res.shape, sh)) {
+    res.has_q = res.has_k = res.has_v = res.has_out = res.has_target = false;
+    res.shape = sh;
+  }
+  if ((!policy.upload_q && !res.has_q) || (!policy.upload_k && !res.has_k) || (!policy.upload_v && !res.has_v) ||
+      (!policy.upload_target && !res.has_target)) {
+    return fail(Status::kInvalidValue, "attention train step: no resident input for a tensor the policy does not upload");
+  }
+  const std::size_t n = sh.elems();
+  const std::size_t bytes = n * sizeof(float);
+  if (policy.upload_q) {
+    LC_TRY(res.q.ensure(bytes));
+    LC_TRY(upload(ctx, res.q.get(), q, bytes));
+    res.has_q = true;
+  }
+  if (policy.upload_k) {
+    LC_TRY(res.k.ensure(bytes));
+    LC_TRY(upload(ctx, res.k.get(), k, bytes));
+    res.has_k = true;
+  }
+  if (policy.upload_v) {
+    LC_TRY(res.v.ensure(bytes));
+    LC_TRY(upload(ctx, res.v.get(), v, bytes));
+    res.has_v = true;
+  }
+  if (policy.upload_target) {
+    LC_TRY(res.target.ensure(bytes));
+    LC_TRY(upload(ctx, res.target.get(), target, bytes));
+    res.has_target = true;
+  }
+  LC_TRY(res.out.ensure(bytes));
+  LC_TRY(res.stats.ensure(sh.seq_len * 2 * sizeof(float)));
+  LC_TRY(res.loss.ensure(sizeof(float)));
+  const int S = static_cast<int>(sh.seq_len);
+  const int D = static_cast<int>(sh.head_dim);
+  // The step's forward has no postprocess (the reference applies it only in
+  // attentionForwardWithPolicy, src/attention.cpp:41-60).
+  hipError_t e = kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(), 1,
+                                    S, D, sh.causal, 1.0f, 0.0f, 0, res.stats.as<float>(), ctx->stream);
+  if (e == hipSuccess && loss_out != nullptr) {
+    e = kern::mseLossF32(res.out.as<float>(), res.target.as<float>(), n,
+                         1.0f / static_cast<float>(sh.seq_len * sh.head_dim), res.loss.as<float>(), ctx->stream);
+  }
+  if (e == hipSuccess) {
+    e = kern::attentionDvUpdateF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(),
+                                   res.target.as<float>(), res.stats.as<float>(), 1, S, D, sh.causal, learning_rate,
+                                   ctx->stream);
+  }
+  if (e != hipSuccess) {
+    return failHip(e, "attention train step launch");
+  }
+  res.has_out = true;
+  if (policy.download_out) {
+    LC_TRY(download(ctx, out, res.out.get(), bytes));
+  }
+  if (policy.download_v) {
+    LC_TRY(download(ctx, v, res.v.get(), bytes));
+  }
+  if (loss_out != nullptr) {
+    LC_TRY(download(ctx, loss_out, res.loss.get(), sizeof(float)));
+  }
+  if (policy.download_out || policy.download_v || loss_out != nullptr || policy.synchronize) {
     LC_TRY(syncStream(ctx));
   }
   return Status::kSuccess;
@@ -176,6 +259,46 @@ Status attentionOneShot(const float* q, const float* k, const float* v, float* o
   return attentionForwardResident(ctx, globalAttnResident(), sh, q, k, v, out, policy, 1);
 }
 
+// src/attention.cpp:12-39 (autoLossEveryForShape / resolveLossEvery).
+int resolveLossEvery(const AttnShape& sh, const lcAttentionIoPolicy& policy) {
+  if (policy.loss_every == 0) {
+    const std::size_t s = sh.seq_len;
+    const std::size_t d = sh.head_dim;
+    if (s == 256 && d == 64) {
+      return 32;
+    }
+    if (s == 256 && d == 128) {
+      return 16;
+    }
+    if ((s == 512 || s == 1024) && (d == 64 || d == 128)) {
+      return 8;
+    }
+    return 4;
+  }
+  return policy.loss_every > 1 ? policy.loss_every : 1;
+}
+
+Status attentionTrainOneShot(const float* q, const float* k, float* v, const float* target, float* out, float lr,
+                             const lcAttentionConfig* cfg, lcDeviceKind device, float* loss_out,
+                             const lcAttentionIoPolicy* policy_in) {
+  if (cfg == nullptr) {
+    return fail(Status::kInvalidValue, "attention train step: null config");
+  }
+  AttnShape sh;
+  sh.seq_len = cfg->seq_len;
+  sh.head_dim = cfg->head_dim;
+  sh.causal = cfg->causal != 0;
+  if (q == nullptr || k == nullptr || v == nullptr || target == nullptr || out == nullptr || sh.seq_len == 0 ||
+      sh.head_dim == 0 || !(lr > 0.0f)) {
+    return fail(Status::kInvalidValue, "attention train step: null pointer, zero dimension or learning_rate <= 0");
+  }
+  HipContext* ctx = nullptr;
+  LC_TRY(requireHip(device, "attention train step", &ctx));
+  const lcAttentionIoPolicy policy = policy_in ? *policy_in : lcAttentionIoPolicyDefault();
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  return attentionTrainResident(ctx, globalAttnResident(), sh, q, k, v, target, out, lr, loss_out, policy);
+}
+
 }  // namespace
 }  // namespace lchip
 
@@ -186,6 +309,11 @@ struct lcAttentionSession {
   lcDeviceKind device = LC_DEVICE_HIP;
   lcAttentionIoPolicy default_policy{};
   AttnResident res;
+  // AttentionSession train state (attention.hpp:120-128): sampled-loss
+  // bookkeeping of trainStepWithPolicy.
+  std::size_t train_step_count = 0;
+  float last_loss = 0.0f;
+  bool has_last_loss = false;
 };
 
 extern "C" {
@@ -360,6 +488,73 @@ lcError_t lcAttentionSessionRunCached(lcAttentionSession* session, size_t repeat
   std::lock_guard<std::recursive_mutex> lock(ctx->mu);
   return toLc(attentionForwardResident(ctx, session->res, session->shape, nullptr, nullptr, nullptr, nullptr, p,
                                        repeat_count));
+}
+
+lcError_t lcAttentionTrainStep(const float* q, const float* k, float* v, const float* target, float* out,
+                               float learning_rate, const lcAttentionConfig* cfg, lcDeviceKind device,
+                               float* loss_out) {
+  return toLc(attentionTrainOneShot(q, k, v, target, out, learning_rate, cfg, device, loss_out, nullptr));
+}
+
+lcError_t lcAttentionTrainStepWithPolicy(const float* q, const float* k, float* v, const float* target, float* out,
+                                         float learning_rate, const lcAttentionConfig* cfg, lcDeviceKind device,
+                                         float* loss_out, const lcAttentionIoPolicy* policy) {
+  if (policy == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "attention train step: null policy"));
+  }
+  return toLc(attentionTrainOneShot(q, k, v, target, out, learning_rate, cfg, device, loss_out, policy));
+}
+
+lcError_t lcAttentionSessionTrainStepWithPolicy(lcAttentionSession* session, const float* q, const float* k,
+                                                float* v, const float* target, float* out, float learning_rate,
+                                                float* loss_out, const lcAttentionIoPolicy* policy) {
+  if (session == nullptr || policy == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "attention session: null session or policy"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(session->device, "attention session train step", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  // src/attention.cpp:298-343: the loss is taken every loss_every steps;
+  // between samples, with nothing downloaded, the step does not block.
+  float sampled = 0.0f;
+  float* effective_loss = nullptr;
+  lcAttentionIoPolicy effective = *policy;
+  if (loss_out != nullptr) {
+    const int every = resolveLossEvery(session->shape, *policy);
+    if (session->train_step_count % static_cast<std::size_t>(every) == 0) {
+      effective_loss = &sampled;
+    } else if (!policy->download_out && !policy->download_v) {
+      effective.synchronize = 0;
+    }
+  }
+  st = attentionTrainResident(ctx, session->res, session->shape, q, k, v, target, out, learning_rate, effective_loss,
+                              effective);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  if (loss_out != nullptr) {
+    if (effective_loss != nullptr) {
+      session->last_loss = sampled;
+      session->has_last_loss = true;
+      *loss_out = sampled;
+    } else {
+      *loss_out = session->has_last_loss ? session->last_loss : 0.0f;
+    }
+  }
+  ++session->train_step_count;
+  return LC_SUCCESS;
+}
+
+lcError_t lcAttentionSessionTrainStep(lcAttentionSession* session, const float* q, const float* k, float* v,
+                                      const float* target, float* out, float learning_rate, float* loss_out) {
+  if (session == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "attention session: null session"));
+  }
+  return lcAttentionSessionTrainStepWithPolicy(session, q, k, v, target, out, learning_rate, loss_out,
+                                               &session->default_policy);
 }
 
 }  // extern "C"

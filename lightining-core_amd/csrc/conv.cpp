@@ -270,7 +270,7 @@ lcError_t lcConvAttentionTorchstrongNchw(const float* x, const float* w, const f
   if (e == hipSuccess) {
     traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, seq_len * seq_len * head_dim);
     e = kern::attentionF32(src, src + need, src + 2 * need, r.attn_out.as<float>(), 1, static_cast<int>(seq_len),
-                           static_cast<int>(head_dim), false, 1.0f, 0.0f, 0, ctx->stream);
+                           static_cast<int>(head_dim), false, 1.0f, 0.0f, 0, nullptr, ctx->stream);
   }
   if (e != hipSuccess) {
     return toLc(failHip(e, "conv_attention launch"));

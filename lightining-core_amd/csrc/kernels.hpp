@@ -54,9 +54,19 @@ hipError_t repeatFillF32(const float* src, size_t n, float* dst, size_t total, h
 hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu, hipStream_t stream);
 
 // Attention over `bh` independent [S, D] fp32 problems (head stride S*D),
-// D <= 256.  Output postprocess relu?(o*post_scale + post_bias).
+// D <= 256.  Output postprocess relu?(o*post_scale + post_bias).  stats
+// (optional, [bh, S, 2]) receives each query's softmax max m and sum l in the
+// log2 domain (p = exp2((q.k)*scale*log2(e) - m) / l).
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D,
-                        bool causal, float post_scale, float post_bias, int post_relu, hipStream_t stream);
+                        bool causal, float post_scale, float post_bias, int post_relu, float* stats,
+                        hipStream_t stream);
+// Train step backward: v -= lr * P^T . (2 (out - target) / (S*D)) per head,
+// P recomputed from q, k and the forward's stats.
+hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const float* out, const float* target,
+                                const float* stats, int bh, int S, int D, bool causal, float lr,
+                                hipStream_t stream);
+// *loss = norm * sum_i (out_i - target_i)^2 (one workgroup, fixed order).
+hipError_t mseLossF32(const float* out, const float* target, size_t n, float norm, float* loss, hipStream_t stream);
 
 // ---- 16-bit ------------------------------------------------------------------
 // dst[b][r][c] = half(src[b][r][c]) for r < rows, c < cols; 0 up to

@@ -37,8 +37,9 @@ template <int DT, int KS, bool VEC>
 __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __restrict__ q,
                                                                const float* __restrict__ k,
                                                                const float* __restrict__ v, float* __restrict__ out,
-                                                               int S, int D, int causal, float scale,
-                                                               float post_scale, float post_bias, int post_relu) {
+                                                               float* __restrict__ stats, int S, int D, int causal,
+                                                               float scale, float post_scale, float post_bias,
+                                                               int post_relu) {
   constexpr int DP = 32 * DT;
   constexpr int KV = 32 * (DP + 1) + 32 * DP;  // floats of one wave's K + V tile
   __shared__ float Qs[32][DP + 1];
@@ -179,6 +180,8 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __re
 
   l_run += __shfl_xor(l_run, 32);
   float inv = 1.0f / l_run;
+  float m_fin = m_run;
+  float l_fin = l_run;
   if constexpr (KS > 1) {
     // Park each wave's state in its own K / V region: m, l (32 each), then
     // O^T as [d][query].  A wave that saw no key tile parks m = -1e30, l = 0.
@@ -212,6 +215,8 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __re
       l_all += f[w] * kv[w][32 + ql];
     }
     inv = 1.0f / l_all;
+    m_fin = m_all;
+    l_fin = l_all;
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
 #pragma unroll
@@ -225,6 +230,12 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __re
         o[t][i] = acc;
       }
     }
+  }
+  // Row statistics for a later pass that recomputes P (the train step's
+  // dV): p = exp2(x - m) / l with x = (q.k) * scale * log2(e).
+  if (stats != nullptr && lane < 32 && qi < S) {
+    stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2] = m_fin;
+    stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2 + 1] = l_fin;
   }
   if (qi < S) {
 #pragma unroll
@@ -244,6 +255,170 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __re
         }
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Train step backward (fp32): dV = P^T . dO with dO = 2 (out - target) / (S*D),
+// then V -= lr * dV in place (the reference's attentionTrainStepCpu,
+// src/attention_cpu.cpp:114-163).  P is not stored: the forward left each
+// query's softmax statistics (m, l), and P[i][j] = exp2(x_ij - m_i) / l_i is
+// recomputed tile by tile from the same x_ij = (q_i.k_j) * scale * log2(e).
+//
+// One workgroup per 32-key block, KS waves splitting its query tiles.  Scores
+// are computed untransposed here, S = Q . K^T, so lane l holds key l % 32 and
+// 16 queries; then dV^T += dO^T . P takes P straight from those registers as
+// the B operand (query order acc_row(s, l) inside each k pair, the same
+// permutation on dO^T).  The KS partial dV^T tiles are summed through LDS in
+// wave order and applied by wave 0.
+// ---------------------------------------------------------------------------
+template <int DT, int KS>
+__global__ __launch_bounds__(64 * KS) void attn_dv_f32_kernel(const float* __restrict__ q,
+                                                              const float* __restrict__ k, float* __restrict__ v,
+                                                              const float* __restrict__ out,
+                                                              const float* __restrict__ target,
+                                                              const float* __restrict__ stats, int S, int D,
+                                                              int causal, float scale, float lr) {
+  constexpr int DP = 32 * DT;
+  constexpr int QO = 32 * (DP + 1) + 32 * DP;  // floats of one wave's Q + dO tile
+  __shared__ float Ks[32][DP + 1];
+  __shared__ __attribute__((aligned(16))) float qo[KS][QO];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  float (*Qs)[DP + 1] = reinterpret_cast<float (*)[DP + 1]>(&qo[wave][0]);
+  float (*Gs)[DP] = reinterpret_cast<float (*)[DP]>(&qo[wave][32 * (DP + 1)]);
+  const int j0 = blockIdx.x * 32;  // first key of this block
+  const size_t head = static_cast<size_t>(blockIdx.y) * S * D;
+  q += head;
+  k += head;
+  v += head;
+  out += head;
+  target += head;
+  stats += static_cast<size_t>(blockIdx.y) * S * 2;
+  const float norm = 1.0f / (static_cast<float>(S) * static_cast<float>(D));
+
+  for (int idx = threadIdx.x; idx < 32 * DP; idx += 64 * KS) {
+    const int r = idx / DP;
+    const int cc = idx - r * DP;
+    Ks[r][cc] = (j0 + r < S && cc < D) ? k[static_cast<size_t>(j0 + r) * D + cc] : 0.0f;
+  }
+  __syncthreads();
+
+  floatx16 dv[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) {
+    dv[t] = zero16();
+  }
+  const int key = j0 + (lane & 31);
+  const int nqt = (S + 31) / 32;
+  // Causal: query tile I meets key block J only when some query >= some key.
+  for (int qt = (causal ? blockIdx.x : 0) + wave; qt < nqt; qt += KS) {
+    const int i0 = qt * 32;
+    for (int idx = lane; idx < 32 * DP; idx += 64) {
+      const int r = idx / DP;
+      const int cc = idx - r * DP;
+      const bool ok = i0 + r < S && cc < D;
+      const size_t off = static_cast<size_t>(i0 + r) * D + cc;
+      Qs[r][cc] = ok ? q[off] : 0.0f;
+      Gs[r][cc] = ok ? 2.0f * (out[off] - target[off]) * norm : 0.0f;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // S = Q . K^T: A = Q rows (query), B = K^T (lane: key, k = d).
+    floatx16 st = zero16();
+#pragma unroll
+    for (int dd = 0; dd < DP; dd += 2) {
+      const float a = Qs[lane & 31][dd + (lane >> 5)];
+      const float b = Ks[lane & 31][dd + (lane >> 5)];
+      st = mfma32x32x2f32(a, b, st);
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = i0 + acc_row(r, lane);
+      float p = 0.0f;
+      if (qi < S && key < S && !(causal && key > qi)) {
+        const float m = stats[static_cast<size_t>(qi) * 2];
+        const float l = stats[static_cast<size_t>(qi) * 2 + 1];
+        p = exp2f((st[r] * scale) * kLog2e - m) / l;
+      }
+      st[r] = p;
+    }
+    // dV^T += dO^T . P: step r pairs queries acc_row(r, l) of both lane halves.
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qr = acc_row(r, lane);
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+        const float a = Gs[qr][t * 32 + (lane & 31)];
+        dv[t] = mfma32x32x2f32(a, st[r], dv[t]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the next query tile overwrites Q / dO
+  }
+
+  // Sum the KS partial dV^T tiles ([d][key]) and update V[key][d].
+  if constexpr (KS > 1) {
+    float* mine = &qo[wave][0];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        mine[(t * 32 + acc_row(r, lane)) * 32 + (lane & 31)] = dv[t][r];
+      }
+    }
+    __syncthreads();
+    if (wave != 0) {
+      return;
+    }
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int idx = (t * 32 + acc_row(r, lane)) * 32 + (lane & 31);
+        float acc = 0.0f;
+#pragma unroll
+        for (int w = 0; w < KS; ++w) {
+          acc += qo[w][idx];
+        }
+        dv[t][r] = acc;
+      }
+    }
+  }
+  if (key < S) {
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int d = t * 32 + acc_row(r, lane);
+        if (d < D) {
+          float* vp = v + static_cast<size_t>(key) * D + d;
+          *vp = *vp - lr * dv[t][r];
+        }
+      }
+    }
+  }
+}
+
+// loss = sum over n elements of (out - target)^2 * norm, one workgroup,
+// fixed reduction order (deterministic).
+__global__ __launch_bounds__(1024) void mse_loss_kernel(const float* __restrict__ out,
+                                                        const float* __restrict__ target, size_t n, float norm,
+                                                        float* __restrict__ loss) {
+  __shared__ float part[1024];
+  float acc = 0.0f;
+  for (size_t i = threadIdx.x; i < n; i += 1024) {
+    const float d = out[i] - target[i];
+    acc += d * d;
+  }
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if (static_cast<int>(threadIdx.x) < w) {
+      part[threadIdx.x] += part[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    *loss = part[0] * norm;
   }
 }
 
@@ -563,7 +738,7 @@ namespace lchip::kern {
 using namespace lchip::k;
 
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D, bool causal,
-                        float post_scale, float post_bias, int post_relu, hipStream_t stream) {
+                        float post_scale, float post_bias, int post_relu, float* stats, hipStream_t stream) {
   if (D <= 0 || D > 256 || S <= 0 || bh <= 0) {
     return hipErrorInvalidValue;
   }
@@ -586,10 +761,10 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
 #define LC_ATTN_F32(DT_, KS_)                                                                                       \
   if (vec && (DT_) <= 2) {                                                                                          \
     hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, ((DT_) <= 2)>), grid, dim3(64 * (KS_)), 0, stream, q, k, v,   \
-                       out, S, D, cz, scale, post_scale, post_bias, post_relu);                                     \
+                       out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);                              \
   } else {                                                                                                          \
-    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out, S,  \
-                       D, cz, scale, post_scale, post_bias, post_relu);                                             \
+    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out,     \
+                       stats, S, D, cz, scale, post_scale, post_bias, post_relu);                                   \
   }
 #define LC_ATTN_F32_KS(DT_)                                                                                         \
   switch (ks) {                                                                                                     \
@@ -610,6 +785,57 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
   }
 #undef LC_ATTN_F32_KS
 #undef LC_ATTN_F32
+  return hipGetLastError();
+}
+
+hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const float* out, const float* target,
+                                const float* stats, int bh, int S, int D, bool causal, float lr,
+                                hipStream_t stream) {
+  if (D <= 0 || D > 256 || S <= 0 || bh <= 0) {
+    return hipErrorInvalidValue;
+  }
+  const float scale = 1.0f / sqrtf(static_cast<float>(D));
+  const int nkb = (S + 31) / 32;
+  const dim3 grid(nkb, bh);
+  const int dt = (D + 31) / 32;
+  const int cz = causal ? 1 : 0;
+  // Query-tile splits: as many as fit (LDS: K tile + per-wave Q / dO tiles)
+  // while the grid stays below about two waves per CU.
+  int ks = 1;
+  while (ks < 8 && static_cast<long long>(nkb) * bh * ks * 2 <= 512 && ks * 2 <= nkb &&
+         (ks * 2) * dt <= (dt <= 2 ? 16 : 8)) {
+    ks *= 2;
+  }
+#define LC_DV_F32(DT_, KS_)                                                                                         \
+  hipLaunchKernelGGL((attn_dv_f32_kernel<DT_, KS_>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out, target, stats, \
+                     S, D, cz, scale, lr)
+#define LC_DV_F32_KS(DT_)                                                                                           \
+  switch (ks) {                                                                                                     \
+    case 8: LC_DV_F32(DT_, (DT_ <= 2 ? 8 : 1)); break;                                                              \
+    case 4: LC_DV_F32(DT_, (DT_ <= 2 ? 4 : 1)); break;                                                              \
+    case 2: LC_DV_F32(DT_, (DT_ <= 4 ? 2 : 1)); break;                                                              \
+    default: LC_DV_F32(DT_, 1); break;                                                                              \
+  }
+  switch (dt) {
+    case 1: LC_DV_F32_KS(1); break;
+    case 2: LC_DV_F32_KS(2); break;
+    case 3: LC_DV_F32_KS(3); break;
+    case 4: LC_DV_F32_KS(4); break;
+    case 5: LC_DV_F32(5, 1); break;
+    case 6: LC_DV_F32(6, 1); break;
+    case 7: LC_DV_F32(7, 1); break;
+    default: LC_DV_F32(8, 1); break;
+  }
+#undef LC_DV_F32_KS
+#undef LC_DV_F32
+  return hipGetLastError();
+}
+
+hipError_t mseLossF32(const float* out, const float* target, size_t n, float norm, float* loss, hipStream_t stream) {
+  if (n == 0) {
+    return hipErrorInvalidValue;
+  }
+  hipLaunchKernelGGL(mse_loss_kernel, dim3(1), dim3(1024), 0, stream, out, target, n, norm, loss);
   return hipGetLastError();
 }
 

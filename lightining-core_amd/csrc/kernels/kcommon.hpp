@@ -102,12 +102,12 @@ __device__ __forceinline__ void load_lds16(const float* src, float* lds_base) {
   __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
 }
 
-// s_waitcnt vmcnt(n) for the small n the pipelines use (expcnt / lgkmcnt
-// left at their maxima; vmcnt's low four bits sit in bits 3:0).
+// s_waitcnt vmcnt(n) (expcnt / lgkmcnt left at their maxima; vmcnt's low
+// four bits sit in bits 3:0 of the immediate, its high two in bits 15:14).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0f70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
 }
 
 // Workgroup barrier without the release fence of __syncthreads(): the fence

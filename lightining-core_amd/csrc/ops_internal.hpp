@@ -26,10 +26,13 @@ struct AttnShape {
 // Device buffers of one attention problem.  fp32 path: q/k/v/out [BH, S, D].
 // 16-bit path: q/k [BH, S_pad, D] and vt [BH, D, S_pad] (zero padded),
 // out fp32 [BH, S, D], stage = fp32 upload staging.
+// Train step (fp32, one head): target [S, D], stats [S, 2] (softmax m, l of
+// the forward), loss one float.
 struct AttnResident {
   AttnShape shape;
   DeviceBuffer q, k, v, out, stage;
-  bool has_q = false, has_k = false, has_v = false, has_out = false;
+  DeviceBuffer target, stats, loss;
+  bool has_q = false, has_k = false, has_v = false, has_out = false, has_target = false;
 };
 
 // Runs one forward on `res` with the reference's policy semantics.
@@ -37,6 +40,14 @@ struct AttnResident {
 Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnShape& shape, const float* q,
                                 const float* k, const float* v, float* out, const lcAttentionIoPolicy& policy,
                                 std::size_t repeat);
+
+// One attention train step on `res` (reference attentionTrainStepWithPolicy,
+// src/attention.cpp:217-244, CPU semantics of attention_cpu.cpp:114-163):
+// forward, loss (when loss_out != nullptr), V -= lr * dV in the resident V,
+// downloads per policy.
+Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShape& shape, const float* q,
+                              const float* k, float* v, const float* target, float* out, float learning_rate,
+                              float* loss_out, const lcAttentionIoPolicy& policy);
 
 // Device buffers of one GEMM, zero padded to the kernel tiles.  fp32:
 // a [roundup(M,64), roundup(K,64)], b [roundup(K,64), roundup(N,64)];

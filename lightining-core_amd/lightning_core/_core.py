@@ -221,6 +221,34 @@ class AttentionSession:
         """Launch-only repeat over the resident inputs, then synchronise."""
         _check(_lib().lcAttentionSessionRunCached(self._h, repeat_count))
 
+    def _train_args(self, q, k, v, target):
+        q, k, v = self._args(q, k, v)
+        target = _f32(target)
+        if target.size != self.numel:
+            raise ValueError("q/k/v/target sizes must match")
+        return q, k, v.copy(), target
+
+    def train_step(self, q, k, v, target, learning_rate: float):
+        """bind_attention.cpp:200-215: returns (out, updated v, loss); the
+        caller's v is not modified (pybind takes it by value)."""
+        q, k, v, target = self._train_args(q, k, v, target)
+        out = np.zeros(self.numel, np.float32)
+        loss = ctypes.c_float(0.0)
+        _check(_lib().lcAttentionSessionTrainStep(self._h, _fp(q), _fp(k), _fp(v), _fp(target), _fp(out),
+                                                  float(learning_rate), ctypes.pointer(loss)))
+        return out, v, float(loss.value)
+
+    def train_step_with_policy(self, q, k, v, target, learning_rate: float, policy: AttentionIoPolicy):
+        """bind_attention.cpp:216-233."""
+        q, k, v, target = self._train_args(q, k, v, target)
+        out = np.zeros(self.numel, np.float32)
+        loss = ctypes.c_float(0.0)
+        c = policy._c()
+        _check(_lib().lcAttentionSessionTrainStepWithPolicy(self._h, _fp(q), _fp(k), _fp(v), _fp(target), _fp(out),
+                                                            float(learning_rate), ctypes.pointer(loss),
+                                                            ctypes.byref(c)))
+        return out, v, float(loss.value)
+
 
 def _require_out(out, n):
     if not isinstance(out, np.ndarray) or out.dtype != np.float32 or not out.flags.c_contiguous:

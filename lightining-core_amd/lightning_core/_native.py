@@ -157,6 +157,11 @@ SIGNATURES = {
     "lcAttentionSessionForward": (_E, [c_void_p, FP, FP, FP, FP]),
     "lcAttentionSessionForwardWithPolicy": (_E, [c_void_p, FP, FP, FP, FP, P(AttentionIoPolicyC)]),
     "lcAttentionSessionRunCached": (_E, [c_void_p, c_size]),
+    "lcAttentionTrainStep": (_E, [FP, FP, FP, FP, FP, c_float, P(AttentionConfig), c_int, FP]),
+    "lcAttentionTrainStepWithPolicy": (_E, [FP, FP, FP, FP, FP, c_float, P(AttentionConfig), c_int, FP,
+                                            P(AttentionIoPolicyC)]),
+    "lcAttentionSessionTrainStep": (_E, [c_void_p, FP, FP, FP, FP, FP, c_float, FP]),
+    "lcAttentionSessionTrainStepWithPolicy": (_E, [c_void_p, FP, FP, FP, FP, FP, c_float, FP, P(AttentionIoPolicyC)]),
     "lcMatMulIoPolicyDefault": (MatMulIoPolicyC, []),
     "lcMatMul": (_E, [FP, FP, FP, c_size, c_size, c_size, c_int]),
     "lcMatMulWithPolicy": (_E, [FP, FP, FP, c_size, c_size, c_size, c_int, P(MatMulIoPolicyC)]),

@@ -127,6 +127,91 @@ int orc_attention_forward_batched(const float* q, const float* k, const float* v
   return ORC_SUCCESS;
 }
 
+/* src/attention_cpu.cpp:114-163 (attentionTrainStepCpu): the forward of
+ * computeAttentionForward keeping the probabilities P [s, s] (same three
+ * passes as orc_attention_forward_rows), then
+ *   diff = out - target; loss += diff*diff (sequential, fp32);
+ *   grad_out = 2*diff*norm with norm = 1/(s*d);
+ *   grad_v[j, c] += P[i, j] * grad_out[i, c]  (j outer, i, c inner);
+ *   v -= learning_rate * grad_v;  loss_out = loss * norm.
+ * No forward postprocess (the reference applies it only in
+ * attentionForwardWithPolicy).  v is updated in place. */
+int orc_attention_train_step(const float* q, const float* k, float* v, const float* target, float* out,
+                             size_t s, size_t d, int causal, float learning_rate, float* loss_out) {
+  if (q == NULL || k == NULL || v == NULL || target == NULL || out == NULL || s == 0 || d == 0) {
+    return ORC_INVALID_VALUE;
+  }
+  float* probs = (float*)malloc(s * s * sizeof(float));
+  float* grad_out = (float*)calloc(s * d, sizeof(float));
+  float* grad_v = (float*)calloc(s * d, sizeof(float));
+  if (probs == NULL || grad_out == NULL || grad_v == NULL) {
+    free(probs);
+    free(grad_out);
+    free(grad_v);
+    return ORC_OUT_OF_MEMORY;
+  }
+  const float scale = 1.0f / sqrtf((float)d);
+  for (size_t i = 0; i < s; ++i) {
+    for (size_t j = 0; j < s; ++j) {
+      probs[i * s + j] = (causal && j > i) ? -1e30f : orc_dot(q + i * d, k + j * d, d) * scale;
+    }
+  }
+  for (size_t i = 0; i < s; ++i) {
+    float* row = probs + i * s;
+    float row_max = row[0];
+    for (size_t j = 1; j < s; ++j) {
+      row_max = fmaxf(row_max, row[j]);
+    }
+    float row_sum = 0.0f;
+    for (size_t j = 0; j < s; ++j) {
+      row[j] = expf(row[j] - row_max);
+      row_sum += row[j];
+    }
+    const float inv = 1.0f / row_sum;
+    for (size_t j = 0; j < s; ++j) {
+      row[j] *= inv;
+    }
+  }
+  memset(out, 0, s * d * sizeof(float));
+  for (size_t i = 0; i < s; ++i) {
+    float* oi = out + i * d;
+    for (size_t j = 0; j < s; ++j) {
+      const float p = probs[i * s + j];
+      const float* vj = v + j * d;
+      for (size_t c = 0; c < d; ++c) {
+        oi[c] += p * vj[c];
+      }
+    }
+  }
+  float loss = 0.0f;
+  const float norm = 1.0f / (float)(s * d);
+  for (size_t i = 0; i < s * d; ++i) {
+    const float diff = out[i] - target[i];
+    loss += diff * diff;
+    grad_out[i] = 2.0f * diff * norm;
+  }
+  for (size_t j = 0; j < s; ++j) {
+    float* gv = grad_v + j * d;
+    for (size_t i = 0; i < s; ++i) {
+      const float p = probs[i * s + j];
+      const float* go = grad_out + i * d;
+      for (size_t c = 0; c < d; ++c) {
+        gv[c] += p * go[c];
+      }
+    }
+  }
+  for (size_t i = 0; i < s * d; ++i) {
+    v[i] -= learning_rate * grad_v[i];
+  }
+  if (loss_out != NULL) {
+    *loss_out = loss * norm;
+  }
+  free(probs);
+  free(grad_out);
+  free(grad_v);
+  return ORC_SUCCESS;
+}
+
 /* src/ops/matmul_cpu.cpp:49-60 (non-Apple branch) for rows [r0, r1):
  * zero-fill, then for i, for p: a = A[i,p]; for j: C[i,j] += a * B[p,j]. */
 int orc_matmul_rows(const float* a, const float* b, float* out, size_t m, size_t k, size_t n,

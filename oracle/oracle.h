@@ -21,6 +21,9 @@
  *                              softmax invariants (constant V, causal row 0,
  *                              q = 0 -> column mean of V)
  *   orc_attention_postprocess  closed form + golden vector
+ *   orc_attention_train_step   golden vectors from the compiled reference,
+ *                              fp64 recomputation of loss / grad_v / update,
+ *                              closed form (V = target-free uniform case)
  *   orc_matmul                 golden vectors, 2x3.3x2 KAT, fp64 brute force
  *   orc_conv2d_nchw            golden vectors, direct-convolution brute force
  *   orc_qkv_pack_repeat        golden vector (conv->attention), closed form
@@ -59,6 +62,12 @@ void orc_attention_postprocess(float* out, size_t n, float scale, float bias, in
  * problems (layout [batch, heads, s, d]). */
 int orc_attention_forward_batched(const float* q, const float* k, const float* v, float* out,
                                   size_t batch, size_t heads, size_t s, size_t d, int causal);
+
+/* src/attention_cpu.cpp:114-163 (attentionTrainStepCpu): forward (out),
+ * mean-squared-error loss against target, grad_v = P^T . grad_out, SGD update
+ * of v in place; *loss_out (if not NULL) = mean of (out - target)^2. */
+int orc_attention_train_step(const float* q, const float* k, float* v, const float* target, float* out,
+                             size_t s, size_t d, int causal, float learning_rate, float* loss_out);
 
 /* src/ops/matmul_cpu.cpp:49-60 (matMulCpu, non-Apple branch). */
 int orc_matmul(const float* a, const float* b, float* out, size_t m, size_t k, size_t n);

@@ -5,6 +5,7 @@
 //
 // Calls (reference file:line):
 //   lightning_core::attentionForwardWithPolicy   src/attention.cpp:137-201
+//   lightning_core::attentionTrainStep           src/attention.cpp:203-214
 //   lightning_core::ops::matMul<float>           include/lightning_core/core/ops.hpp:195-205
 //   lightning_core::ops::conv2dNchw<float>       include/lightning_core/core/ops.hpp:855-1213
 // all with Device::kCPU.
@@ -26,6 +27,15 @@ int ref_attention_forward(const float* q, const float* k, const float* v, float*
   policy.output_bias = out_bias;
   policy.output_relu = out_relu != 0;
   return static_cast<int>(lc::attentionForwardWithPolicy(q, k, v, out, cfg, lc::runtime::Device::kCPU, policy));
+}
+
+// attentionTrainStep (src/attention.cpp:203-214) on the CPU device: v is
+// updated in place, *loss receives the mean squared error.
+int ref_attention_train_step(const float* q, const float* k, float* v, const float* target, float* out, size_t s,
+                             size_t d, int causal, float learning_rate, float* loss) {
+  lc::AttentionConfig cfg{s, d, causal != 0};
+  return static_cast<int>(
+      lc::attentionTrainStep(q, k, v, target, out, learning_rate, cfg, lc::runtime::Device::kCPU, loss));
 }
 
 int ref_matmul(const float* a, const float* b, float* out, size_t m, size_t k, size_t n) {

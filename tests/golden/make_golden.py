@@ -39,6 +39,7 @@ def _load_ref():
     lib = ctypes.CDLL(path)
     lib.ref_attention_forward.argtypes = [_P, _P, _P, _P, _S, _S, ctypes.c_int, ctypes.c_float, ctypes.c_float,
                                           ctypes.c_int]
+    lib.ref_attention_train_step.argtypes = [_P, _P, _P, _P, _P, _S, _S, ctypes.c_int, ctypes.c_float, _P]
     lib.ref_matmul.argtypes = [_P, _P, _P, _S, _S, _S]
     lib.ref_conv2d_nchw.argtypes = [_P, _P, _P, _P] + [_S] * 11 + [ctypes.c_int]
     lib.ref_conv_attention.argtypes = [_P, _P, _P, _P] + [_S] * 13
@@ -72,6 +73,20 @@ def attention_case(lib, name, q, k, v, s, d, causal, scale=1.0, bias=0.0, relu=F
     assert st == 0, st
     _dump(name, {"op": "attention", "seq_len": s, "head_dim": d, "causal": bool(causal), "output_scale": scale,
                  "output_bias": bias, "output_relu": bool(relu)}, {"q": q, "k": k, "v": v}, out)
+
+
+def train_case(lib, name, q, k, v, target, s, d, causal, lr):
+    """attentionTrainStep: expected = out (s*d) ++ updated v (s*d) ++ [loss]."""
+    q, k, v0, target = _f32(q), _f32(k), _f32(v), _f32(target)
+    v = v0.copy()
+    out = np.zeros(s * d, np.float32)
+    loss = np.zeros(1, np.float32)
+    st = lib.ref_attention_train_step(_ptr(q), _ptr(k), _ptr(v), _ptr(target), _ptr(out), s, d, int(causal),
+                                      lr, _ptr(loss))
+    assert st == 0, st
+    _dump(name, {"op": "attention_train_step", "seq_len": s, "head_dim": d, "causal": bool(causal),
+                 "learning_rate": lr, "expected_layout": ["out", "v", "loss"]},
+          {"q": q, "k": k, "v": v0, "target": target}, np.concatenate([out.ravel(), v.ravel(), loss]))
 
 
 def matmul_case(lib, name, a, b, m, k, n):
@@ -126,6 +141,19 @@ def main():
         k = synth.normal((s, d), seed=7, stream=2)
         v = synth.normal((s, d), seed=7, stream=3)
         attention_case(lib, f"attention_normal_s{s}_d{d}{'_causal' if causal else ''}", q, k, v, s, d, causal)
+
+    # Train step (attentionTrainStep, src/attention.cpp:203-214): the
+    # reference's makeValue inputs with a makeValue target, plus seeded odd
+    # shapes, causal and not.
+    n = 16 * 32
+    train_case(lib, "train_attention_makevalue_s16_d32", qv, kv, vv, mv(n, 0.007, 0.03), 16, 32, False, 0.05)
+    for s, d, causal, lr in [(33, 20, True, 0.1), (70, 64, False, 0.01), (64, 128, True, 0.5)]:
+        q = synth.normal((s, d), seed=9, stream=1)
+        k = synth.normal((s, d), seed=9, stream=2)
+        v = synth.normal((s, d), seed=9, stream=3)
+        t = synth.normal((s, d), seed=9, stream=4)
+        train_case(lib, f"train_attention_normal_s{s}_d{d}{'_causal' if causal else ''}", q, k, v, t, s, d, causal,
+                   lr)
 
     # tests/test_matmul.cpp:14-50 known answer; test_backend_parity.cpp:66-89.
     matmul_case(lib, "matmul_kat_2x3x2", np.arange(1, 7, dtype=np.float32), np.arange(7, 13, dtype=np.float32),

@@ -35,6 +35,7 @@ class Oracle:
         lib.orc_attention_postprocess.argtypes = [_P, _S, _F, _F, _I]
         lib.orc_attention_postprocess.restype = None
         lib.orc_attention_forward_batched.argtypes = [_P, _P, _P, _P, _S, _S, _S, _S, _I]
+        lib.orc_attention_train_step.argtypes = [_P, _P, _P, _P, _P, _S, _S, _I, _F, _P]
         lib.orc_matmul.argtypes = [_P, _P, _P, _S, _S, _S]
         lib.orc_matmul_rows.argtypes = [_P, _P, _P, _S, _S, _S, _S, _S]
         lib.orc_conv2d_nchw.argtypes = [_P, _P, _P, _P] + [_S] * 11 + [_I]
@@ -55,6 +56,18 @@ class Oracle:
         st = self.lib.orc_attention_forward_rows(_ptr(q), _ptr(k), _ptr(v), _ptr(out), s, d, int(causal), r0, r1)
         assert st == 0, st
         return out
+
+    def attention_train_step(self, q, k, v, target, lr, causal=False):
+        """Returns (out, updated v, loss); the inputs are not modified."""
+        q, k, target = self._c(q), self._c(k), self._c(target)
+        v = self._c(v).copy()
+        s, d = q.shape
+        out = np.zeros((s, d), np.float32)
+        loss = np.zeros(1, np.float32)
+        st = self.lib.orc_attention_train_step(_ptr(q), _ptr(k), _ptr(v), _ptr(target), _ptr(out), s, d,
+                                               int(causal), lr, _ptr(loss))
+        assert st == 0, st
+        return out, v, float(loss[0])
 
     def postprocess(self, out, scale, bias, relu):
         out = self._c(out).copy()

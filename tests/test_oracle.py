@@ -204,6 +204,62 @@ def test_vit_block_composition(oracle):
     np.testing.assert_array_equal(oracle.vit_block(x, w_conv, w_qkv, w_o, heads, rows=(10, 30)), got[10:30])
 
 
+# --- attention train step (src/attention_cpu.cpp:114-163) -----------------------
+
+def _bf_train_step(q, k, v, t, lr, causal):
+    """float64: forward, mean squared error, grad_v = P^T . 2(out - t)/(S*D), SGD."""
+    q, k, v, t = (np.asarray(x, np.float64) for x in (q, k, v, t))
+    s, d = q.shape
+    sc = q @ k.T / np.sqrt(d)
+    if causal:
+        sc = np.where(np.triu(np.ones((s, s), bool), 1), -np.inf, sc)
+    p = np.exp(sc - sc.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    out = p @ v
+    go = 2.0 * (out - t) / (s * d)
+    return out, v - lr * (p.T @ go), float(np.mean((out - t) ** 2))
+
+
+@pytest.mark.parametrize("case", oracle_lib.golden_cases("train_attention"), ids=lambda c: c["name"])
+def test_train_step_golden(oracle, case):
+    p = case["params"]
+    s, d = p["seq_len"], p["head_dim"]
+    q, k, v, t = (oracle_lib.golden_input(case, n).reshape(s, d) for n in ("q", "k", "v", "target"))
+    out, v_new, loss = oracle.attention_train_step(q, k, v, t, p["learning_rate"], p["causal"])
+    exp = np.asarray(case["expected"], np.float32)
+    assert oracle_lib.normwise_rel(exp[:s * d], out.ravel()) <= GOLD_TOL
+    assert oracle_lib.normwise_rel(exp[s * d:2 * s * d], v_new.ravel()) <= GOLD_TOL
+    assert abs(loss - exp[-1]) <= GOLD_TOL * abs(exp[-1])
+
+
+@pytest.mark.parametrize("s,d,causal,lr", [(17, 8, False, 5.0), (40, 33, True, 20.0), (64, 64, True, 50.0)])
+def test_train_step_bruteforce(oracle, s, d, causal, lr):
+    # learning rates large enough that the update (~lr * 2|out - t| / (S*D))
+    # dwarfs the fp32 rounding of v itself, so the update is checked on its own
+    q, k, v, t = (synth.normal((s, d), seed=40, stream=i) for i in range(4))
+    out, v_new, loss = oracle.attention_train_step(q, k, v, t, lr, causal)
+    bo, bv, bl = _bf_train_step(q, k, v, t, lr, causal)
+    assert oracle_lib.normwise_rel(bo, out) <= 1e-5
+    upd = bv - np.asarray(v, np.float64)
+    assert np.max(np.abs(np.asarray(v_new, np.float64) - bv)) <= 1e-3 * np.max(np.abs(upd))
+    assert abs(loss - bl) <= 1e-5 * bl
+
+
+def test_train_step_closed_form(oracle):
+    # q = 0: P is uniform (1/S), out = column mean of V for every row; with
+    # target 0 the loss is mean(out^2) and every row of grad_v is the same,
+    # 2/(S*S*D) * sum_i out_i = 2/(S*D) * colmean(V).
+    s, d, lr = 12, 5, 0.25
+    v = synth.normal((s, d), seed=41, stream=1)
+    out, v_new, loss = oracle.attention_train_step(np.zeros((s, d)), synth.normal((s, d), seed=41, stream=2), v,
+                                                   np.zeros((s, d)), lr)
+    cm = np.asarray(v, np.float64).mean(axis=0)
+    np.testing.assert_allclose(out, np.tile(cm, (s, 1)), rtol=1e-5, atol=1e-6)
+    assert abs(loss - float(np.mean(cm ** 2))) <= 1e-5 * float(np.mean(cm ** 2))
+    np.testing.assert_allclose(v_new, np.asarray(v, np.float64) - lr * 2.0 / (s * d) * cm[None, :], rtol=1e-5,
+                               atol=1e-6)
+
+
 # --- sensitivity: planted mistakes are caught -----------------------------------
 
 def test_checks_catch_planted_mistakes(oracle):
@@ -219,3 +275,15 @@ def test_checks_catch_planted_mistakes(oracle):
     x, w = synth.normal((1, 2, 6, 6), seed=32, stream=1), synth.normal((3, 2, 3, 3), seed=32, stream=2)
     flipped = oracle.conv2d(x, w[:, :, ::-1, ::-1].copy(), None, (1, 1), (1, 1))
     assert oracle_lib.normwise_rel(_direct_conv(x, w, None, (1, 1), (1, 1), False), flipped) > 1e-2
+    # train step: a sign error in the update and an untransposed P are caught
+    t = synth.normal((s, d), seed=30, stream=5)
+    _, bv, _ = _bf_train_step(q, k, v, t, 0.5, True)
+    _, v_neg, _ = oracle.attention_train_step(q, k, v, t, -0.5, True)
+    assert oracle_lib.normwise_rel(bv - v, np.asarray(v_neg, np.float64) - v) > 1e-2
+    qq, kk = np.asarray(q, np.float64), np.asarray(k, np.float64)
+    sc = np.where(np.triu(np.ones((s, s), bool), 1), -np.inf, qq @ kk.T / np.sqrt(d))
+    pm = np.exp(sc - sc.max(axis=1, keepdims=True))
+    pm /= pm.sum(axis=1, keepdims=True)
+    go = 2.0 * (pm @ np.asarray(v, np.float64) - t) / (s * d)
+    _, v_ok, _ = oracle.attention_train_step(q, k, v, t, 0.5, True)
+    assert oracle_lib.normwise_rel(-0.5 * (pm @ go), np.asarray(v_ok, np.float64) - v) > 1e-2
