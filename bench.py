@@ -71,11 +71,13 @@ class CpuBaseline:
             self.lib.ref_matmul.argtypes = [P, P, P, S, S, S]
             self.lib.ref_attention_forward.argtypes = [P, P, P, P, S, S, ctypes.c_int, ctypes.c_float,
                                                        ctypes.c_float, ctypes.c_int]
+            self.lib.ref_attention_train_step.argtypes = [P, P, P, P, P, S, S, ctypes.c_int, ctypes.c_float, P]
         if os.path.exists(orc):
             self.orc = ctypes.CDLL(orc)
             self.orc.orc_matmul_rows.argtypes = [P, P, P, S, S, S, S, S]
             self.orc.orc_attention_forward_rows.argtypes = [P, P, P, P, S, S, ctypes.c_int, S, S]
             self.orc.orc_vit_block.argtypes = [P] * 5 + [S] * 9
+            self.orc.orc_attention_train_step.argtypes = [P, P, P, P, P, S, S, ctypes.c_int, ctypes.c_float, P]
             if self.lib is None:
                 self.kind = "port"
         else:
@@ -115,6 +117,15 @@ class CpuBaseline:
             self.orc.orc_attention_forward_rows(self._p(q), self._p(k), self._p(v), self._p(out), s, d, int(causal),
                                                 0, s)
         return out
+
+    def attention_train_step(self, q, k, v, t, lr, causal):
+        """One step; v is updated in place, returns the loss."""
+        s, d = q.shape
+        out = np.empty_like(q)
+        loss = np.zeros(1, np.float32)
+        fn = self.lib.ref_attention_train_step if self.kind == "reference" else self.orc.orc_attention_train_step
+        fn(self._p(q), self._p(k), self._p(v), self._p(t), self._p(out), s, d, int(causal), lr, self._p(loss))
+        return float(loss[0])
 
     def attention_rows(self, q, k, v, causal, r0, r1):
         s, d = q.shape
@@ -229,6 +240,40 @@ def bench_extras(lc, synth, cpu):
         cpu_tf = round(n * 4.0 * s * s * d / el / 1e12, 6)
         sample = f"{n} full forwards in {el:.2f} s, 1 thread ({cpu.kind})"
     out["C1_attention_f32_S256_D64"] = extra_entry("C1", 4.0 * s * s * d, ms, "f32", cpu_tf, sample)
+    sess.close()
+
+    # T1 attention train step fp32 S=256 D=64 (the
+    # reference's training shape, loss sampled every 32 steps as its
+    # shape-aware default): V stays resident, nothing is downloaded.
+    # Algorithmic work 6*S^2*D (forward 4, P^T . dO 2); the kernels also
+    # recompute Q.K^T for the backward (another 2*S^2*D, not counted).
+    q, k, v, t = (synth.normal((s, d), stream=205 + i) for i in range(4))
+    sess = lc.AttentionSession(s, d, causal=False)
+    lr = 0.5
+    sess.train_step_with_policy(q, k, v, t, lr, lc.AttentionIoPolicy(download_out=False, download_v=False,
+                                                                      synchronize=False, loss_every=0))
+    keep = lc.AttentionIoPolicy(upload_q=False, upload_k=False, upload_v=False, upload_target=False,
+                                download_out=False, download_v=False, synchronize=False, loss_every=0)
+
+    def train_loop(n):
+        for _ in range(n):
+            sess.train_step_with_policy(q, k, v, t, lr, keep)
+
+    train_loop(32)
+    iters = 256
+    ms = timed(lc, train_loop, iters) / iters
+    cpu_tf = sample = None
+    if cpu.kind is not None:
+        vc = np.array(v, np.float32)
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < 1.0:
+            cpu.attention_train_step(q, k, vc, t, lr, False)
+            n += 1
+        el = time.perf_counter() - t0
+        cpu_tf = round(n * 6.0 * s * s * d / el / 1e12, 6)
+        sample = f"{n} full train steps in {el:.2f} s, 1 thread ({cpu.kind})"
+    out["T1_attention_train_f32_S256_D64"] = extra_entry("T1", 6.0 * s * s * d, ms, "f32", cpu_tf, sample)
     sess.close()
 
     # C3 attention bf16 causal B4 H16 S2048 D128
