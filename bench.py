@@ -72,6 +72,7 @@ class CpuBaseline:
             self.lib.ref_attention_forward.argtypes = [P, P, P, P, S, S, ctypes.c_int, ctypes.c_float,
                                                        ctypes.c_float, ctypes.c_int]
             self.lib.ref_attention_train_step.argtypes = [P, P, P, P, P, S, S, ctypes.c_int, ctypes.c_float, P]
+            self.lib.ref_conv_attention.argtypes = [P, P, P, P] + [S] * 13
         if os.path.exists(orc):
             self.orc = ctypes.CDLL(orc)
             self.orc.orc_matmul_rows.argtypes = [P, P, P, S, S, S, S, S]
@@ -126,6 +127,15 @@ class CpuBaseline:
         fn = self.lib.ref_attention_train_step if self.kind == "reference" else self.orc.orc_attention_train_step
         fn(self._p(q), self._p(k), self._p(v), self._p(t), self._p(out), s, d, int(causal), lr, self._p(loss))
         return float(loss[0])
+
+    def conv_attention(self, x, w, bias, seq, hd, pad):
+        """The reference's conv -> QKV repeat -> attention chain (reference kind only)."""
+        bn, c, h, wd = x.shape
+        oc, _, kh, kw = w.shape
+        out = np.empty(seq * hd, np.float32)
+        self.lib.ref_conv_attention(self._p(x), self._p(w), self._p(bias), self._p(out), bn, c, h, wd, oc, kh, kw,
+                                    seq, hd, 1, 1, pad, pad)
+        return out
 
     def attention_rows(self, q, k, v, causal, r0, r1):
         s, d = q.shape
@@ -300,6 +310,39 @@ def bench_extras(lc, synth, cpu):
     out["C3_attention_bf16_causal_B4_H16_S2048_D128"] = extra_entry("C3", flops, ms, "bf16", cpu_tf, sample)
     sess.close()
     del q, k, v
+
+    # the reference's conv -> attention hotspot shapes
+    # (README.md Pipeline Bench, "Integrated API ms" column: 0.396-0.431 ms on
+    # its Apple GPU): conv n=1 c=3->16 h=w=8 k=3 pad 1 + ReLU, QkvPackRepeat,
+    # attention.  One integrated API call per step, host arrays in and out, so
+    # the time includes both PCIe copies (the fused conv+attention kernel is
+    # one launch).
+    for seq, hd, ref_ms in [(48, 48, 0.404033), (192, 48, 0.415871), (192, 8, 0.407752), (96, 48, 0.398017)]:
+        x = synth.normal((1, 3, 8, 8), stream=230)
+        w = synth.normal((16, 3, 3, 3), std=0.3, stream=231)
+        b = synth.normal((16,), stream=232)
+        for _ in range(20):
+            lc.api.conv_attention_torchstrong_nchw(x, w, b, seq, hd, 1, 1, 1, 1)
+        iters = 300
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            lc.api.conv_attention_torchstrong_nchw(x, w, b, seq, hd, 1, 1, 1, 1)
+        ms = (time.perf_counter() - t0) * 1e3 / iters
+        flops = 2.0 * 64 * 16 * 27 + 4.0 * seq * seq * hd
+        entry = {"ms_per_call": round(ms, 5), "includes": "H2D of x/w/bias, fused kernel, D2H of out, sync",
+                 "TFLOP/s": round(flops / (ms * 1e-3) / 1e12, 4),
+                 "reference_published_integrated_api_ms": ref_ms}
+        if cpu.kind == "reference":
+            t0 = time.perf_counter()
+            n = 0
+            while time.perf_counter() - t0 < 0.5:
+                cpu.conv_attention(x, w, b, seq, hd, 1)
+                n += 1
+            el = time.perf_counter() - t0
+            entry["cpu_ms_per_call"] = round(el * 1e3 / n, 5)
+            entry["cpu_sample"] = f"{n} calls in {el:.2f} s, 1 thread (reference)"
+        log(f"[bench] P conv->attn seq={seq} d={hd}: {entry}")
+        out[f"P_conv_attn_c3_16_h8_seq{seq}_d{hd}"] = entry
 
     # C4 ViT block fp16
     bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12

@@ -14,6 +14,7 @@
 //    the epilogues: implicit-GEMM patch-embed conv (+ReLU) writing tokens
 //    [B*T, E]; QKV GEMM writing head-major Q/K and transposed V; flash
 //    attention writing heads concatenated [B*T, E]; output projection.
+#include <algorithm>
 #include <cstring>
 #include <map>
 #include <string>
@@ -247,11 +248,60 @@ lcError_t lcConvAttentionTorchstrongNchw(const float* x, const float* w, const f
   }
   std::lock_guard<std::recursive_mutex> lock(ctx->mu);
   ConvResident& r = globalConv();
+  const std::size_t need = seq_len * head_dim;
+  if (g.outSize() <= 8192 && 3 * need < (std::size_t{1} << 31)) {
+    // The reference's hotspot shapes (small conv, repeated into Q/K/V): one
+    // fused launch, conv recomputed per workgroup into LDS.
+    // x, w and bias go over in one DMA copy from pinned staging (these calls
+    // are small enough that per-copy overhead is most of their time), and
+    // the output comes back the same way.
+    const std::size_t xs = g.batch * g.in_c * g.in_h * g.in_w;
+    const std::size_t ws = g.out_c * g.kin();
+    const std::size_t bs = bias != nullptr ? g.out_c : 0;
+    const std::size_t in_floats = xs + ws + bs;
+    st = r.x.ensure(in_floats * sizeof(float));
+    if (st == Status::kSuccess) st = r.attn_out.ensure(need * sizeof(float));
+    if (st == Status::kSuccess) st = ctx->pinned.ensure(std::max(in_floats, need) * sizeof(float));
+    if (st != Status::kSuccess) {
+      return toLc(st);
+    }
+    float* stage = static_cast<float*>(ctx->pinned.get());
+    std::memcpy(stage, x, xs * sizeof(float));
+    std::memcpy(stage + xs, w, ws * sizeof(float));
+    if (bs != 0) {
+      std::memcpy(stage + xs + ws, bias, bs * sizeof(float));
+    }
+    st = upload(ctx, r.x.get(), stage, in_floats * sizeof(float));
+    if (st != Status::kSuccess) {
+      return toLc(st);
+    }
+    const float* dx = r.x.as<float>();
+    const float* dw = dx + xs;
+    const float* dbias = bs != 0 ? dx + xs + ws : nullptr;
+    traceOpDispatch(TraceOp::kConv2dNchw, Device::kHIP, Device::kHIP, false, g.rows() * g.out_c * g.kin());
+    traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, seq_len * seq_len * head_dim);
+    const hipError_t e = kern::convAttentionF32(
+        dx, dw, dbias, static_cast<int>(g.batch), static_cast<int>(g.in_c),
+        static_cast<int>(g.in_h), static_cast<int>(g.in_w), static_cast<int>(g.out_c), static_cast<int>(g.kh),
+        static_cast<int>(g.kw), static_cast<int>(g.sh), static_cast<int>(g.sw), static_cast<int>(g.ph),
+        static_cast<int>(g.pw), static_cast<int>(seq_len), static_cast<int>(head_dim), r.attn_out.as<float>(),
+        ctx->stream);
+    if (e != hipSuccess) {
+      return toLc(failHip(e, "conv_attention launch"));
+    }
+    st = download(ctx, stage, r.attn_out.get(), need * sizeof(float));
+    if (st == Status::kSuccess) {
+      st = syncStream(ctx);
+    }
+    if (st == Status::kSuccess) {
+      std::memcpy(out, stage, need * sizeof(float));
+    }
+    return toLc(st);
+  }
   st = convForwardDevice(ctx, r, g, x, w, bias, true);
   if (st != Status::kSuccess) {
     return toLc(st);
   }
-  const std::size_t need = seq_len * head_dim;
   const std::size_t total = 3 * need;
   const float* src = r.out.as<float>();
   hipError_t e = hipSuccess;

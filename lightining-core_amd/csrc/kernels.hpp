@@ -60,6 +60,14 @@ hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu,
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D,
                         bool causal, float post_scale, float post_bias, int post_relu, float* stats,
                         hipStream_t stream);
+// The reference's conv -> attention chain in one launch: conv2d NCHW (+bias,
+// ReLU) of x [batch, cin, h, wd] with w [cout, cin, kh, kw], Q/K/V = the
+// consecutive S*D slices of its flat output repeated to 3*S*D values, then
+// single-head non-causal attention -> out [S, D].  The conv output must have
+// at most 8192 values.
+hipError_t convAttentionF32(const float* x, const float* w, const float* bias, int batch, int cin, int h, int wd,
+                            int cout, int kh, int kw, int sh, int sw, int ph, int pw, int S, int D, float* out,
+                            hipStream_t stream);
 // Train step backward: v -= lr * P^T . (2 (out - target) / (S*D)) per head,
 // P recomputed from q, k and the forward's stats.
 hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const float* out, const float* target,

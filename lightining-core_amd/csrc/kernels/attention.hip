@@ -33,17 +33,122 @@ constexpr float kMaskValue = -1e30f;
 // rescaled by exp2(m_w - m) and summed in wave order).  KS > 1 puts more
 // waves on small problems (one head of S = 256 is 8 query blocks).
 // ---------------------------------------------------------------------------
-template <int DT, int KS, bool VEC>
-__global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __restrict__ q,
-                                                               const float* __restrict__ k,
-                                                               const float* __restrict__ v, float* __restrict__ out,
+// Where the fp32 attention kernel reads Q, K and V (element i of the
+// [BH, S, D] layout).  kLds: floats of LDS the source keeps; kVec: K and V
+// rows are plain 16-byte aligned global memory (float4 prefetch allowed).
+struct AttnSrcGlobal {
+  const float* q;
+  const float* k;
+  const float* v;
+  static constexpr int kLds = 0;
+  static constexpr bool kVec = true;
+  __device__ void prologue(float*, int) const {}
+  __device__ float ldq(const float*, size_t i) const { return q[i]; }
+  __device__ float ldk(const float*, size_t i) const { return k[i]; }
+  __device__ float ldv(const float*, size_t i) const { return v[i]; }
+};
+
+// The reference's conv -> attention chain (bind_integrated.cpp:614-730):
+// conv2d NCHW + bias + ReLU, then Q, K, V = consecutive S*D slices of the
+// flat conv output, tiled by repetition when it holds fewer than 3*S*D values
+// (QkvPackRepeat, :709-729).  Each workgroup computes the whole conv output
+// (n <= kOut values) into LDS once, accumulating over (c, ky, kx) in im2col
+// column order and adding the bias last as the reference's GEMM + scatter
+// does; Q / K / V are then read from it by index.
+struct AttnSrcConvRepeat {
+  const float* x;
+  const float* w;
+  const float* bias;
+  int cin, h, wd, cout, kh, kw, sh, sw, ph, pw, oh, ow;
+  int n;        // conv output values (batch * cout * oh * ow), at most kOut
+  int xs, ws;   // input and weight values
+  size_t need;  // S * D
+  static constexpr int kOut = 8192;
+  static constexpr int kLds = 12288;
+  static constexpr bool kVec = false;
+  __device__ void prologue(float* buf, int nthreads) const {
+    // x and w are staged behind the output when they fit (one coalesced pass
+    // instead of a dependent global load per multiply-add).
+    const bool staged = n + xs + ws <= kLds;
+    const float* xp = x;
+    const float* wp = w;
+    if (staged) {
+      float* xb = buf + n;
+      float* wb = xb + xs;
+      for (int i = threadIdx.x; i < xs; i += nthreads) {
+        xb[i] = x[i];
+      }
+      for (int i = threadIdx.x; i < ws; i += nthreads) {
+        wb[i] = w[i];
+      }
+      __syncthreads();
+      xp = xb;
+      wp = wb;
+    }
+    for (int f = threadIdx.x; f < n; f += nthreads) {
+      const int ox = f % ow;
+      int t = f / ow;
+      const int oy = t % oh;
+      t /= oh;
+      const int oc = t % cout;
+      const int b = t / cout;
+      float acc = 0.0f;
+      for (int c = 0; c < cin; ++c) {
+        const float* xc = xp + (static_cast<size_t>(b) * cin + c) * h * wd;
+        const float* wc = wp + (static_cast<size_t>(oc) * cin + c) * kh * kw;
+        if (kh == 3 && kw == 3) {
+          // the hotspot kernel size: all nine loads issued together
+#pragma unroll
+          for (int ky = 0; ky < 3; ++ky) {
+            const int iy = oy * sh + ky - ph;
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+              const int ix = ox * sw + kx - pw;
+              const float xv = (iy >= 0 && iy < h && ix >= 0 && ix < wd) ? xc[iy * wd + ix] : 0.0f;
+              acc += xv * wc[ky * 3 + kx];
+            }
+          }
+          continue;
+        }
+        for (int ky = 0; ky < kh; ++ky) {
+          const int iy = oy * sh + ky - ph;
+          for (int kx = 0; kx < kw; ++kx) {
+            const int ix = ox * sw + kx - pw;
+            const float xv = (iy >= 0 && iy < h && ix >= 0 && ix < wd) ? xc[iy * wd + ix] : 0.0f;
+            acc += xv * wc[ky * kw + kx];
+          }
+        }
+      }
+      if (bias != nullptr) {
+        acc += bias[oc];
+      }
+      buf[f] = acc > 0.0f ? acc : 0.0f;
+    }
+    __syncthreads();
+  }
+  // 32-bit index arithmetic (the host keeps 3*S*D below 2^31).
+  __device__ float ldq(const float* buf, size_t i) const {
+    return buf[static_cast<uint32_t>(i) % static_cast<uint32_t>(n)];
+  }
+  __device__ float ldk(const float* buf, size_t i) const {
+    return buf[static_cast<uint32_t>(need + i) % static_cast<uint32_t>(n)];
+  }
+  __device__ float ldv(const float* buf, size_t i) const {
+    return buf[static_cast<uint32_t>(2 * need + i) % static_cast<uint32_t>(n)];
+  }
+};
+
+template <int DT, int KS, bool VEC, typename Src>
+__global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* __restrict__ out,
                                                                float* __restrict__ stats, int S, int D, int causal,
                                                                float scale, float post_scale, float post_bias,
                                                                int post_relu) {
   constexpr int DP = 32 * DT;
   constexpr int KV = 32 * (DP + 1) + 32 * DP;  // floats of one wave's K + V tile
+  static_assert(!VEC || Src::kVec, "vector prefetch needs a global source");
   __shared__ float Qs[32][DP + 1];
   __shared__ __attribute__((aligned(16))) float kv[KS][KV];
+  __shared__ float srcbuf[Src::kLds > 0 ? Src::kLds : 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   float (*Ks)[DP + 1] = reinterpret_cast<float (*)[DP + 1]>(&kv[wave][0]);
@@ -52,15 +157,13 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __re
   const int qb = nqb - 1 - static_cast<int>(blockIdx.x);  // heaviest (causal) blocks first
   const int q0 = qb * 32;
   const size_t head = static_cast<size_t>(blockIdx.y) * S * D;
-  q += head;
-  k += head;
-  v += head;
   out += head;
+  src.prologue(srcbuf, 64 * KS);
 
   for (int idx = threadIdx.x; idx < 32 * DP; idx += 64 * KS) {
     const int r = idx / DP;
     const int c = idx - r * DP;
-    Qs[r][c] = (q0 + r < S && c < D) ? q[static_cast<size_t>(q0 + r) * D + c] : 0.0f;
+    Qs[r][c] = (q0 + r < S && c < D) ? src.ldq(srcbuf, head + static_cast<size_t>(q0 + r) * D + c) : 0.0f;
   }
   __syncthreads();
 
@@ -89,8 +192,10 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __re
       const int cc = (idx - r * (DP / 4)) * 4;
       const bool ok = j0 + r < S && cc < D;
       const size_t off = static_cast<size_t>(j0 + r) * D + cc;
-      kr[c] = ok ? *reinterpret_cast<const float4*>(k + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      vr[c] = ok ? *reinterpret_cast<const float4*>(v + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      if constexpr (VEC) {
+        kr[c] = ok ? *reinterpret_cast<const float4*>(src.k + head + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        vr[c] = ok ? *reinterpret_cast<const float4*>(src.v + head + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     }
   };
   if constexpr (VEC) {
@@ -115,12 +220,14 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(const float* __re
         fetch(j0 + 32 * KS);
       }
     } else {
+#pragma unroll 8
       for (int idx = lane; idx < 32 * DP; idx += 64) {
         const int r = idx / DP;
         const int cc = idx - r * DP;
         const bool ok = (j0 + r < S && cc < D);
-        Ks[r][cc] = ok ? k[static_cast<size_t>(j0 + r) * D + cc] : 0.0f;
-        Vs[r][cc] = ok ? v[static_cast<size_t>(j0 + r) * D + cc] : 0.0f;
+        const size_t off = head + static_cast<size_t>(j0 + r) * D + cc;
+        Ks[r][cc] = ok ? src.ldk(srcbuf, off) : 0.0f;
+        Vs[r][cc] = ok ? src.ldv(srcbuf, off) : 0.0f;
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -758,13 +865,14 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
   }
   const bool vec = dt <= 2 && D % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(v) % 16 == 0;
+  const AttnSrcGlobal src{q, k, v};
 #define LC_ATTN_F32(DT_, KS_)                                                                                       \
   if (vec && (DT_) <= 2) {                                                                                          \
-    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, ((DT_) <= 2)>), grid, dim3(64 * (KS_)), 0, stream, q, k, v,   \
-                       out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);                              \
+    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, ((DT_) <= 2), AttnSrcGlobal>), grid, dim3(64 * (KS_)), 0,    \
+                       stream, src, out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);                 \
   } else {                                                                                                          \
-    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out,     \
-                       stats, S, D, cz, scale, post_scale, post_bias, post_relu);                                   \
+    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false, AttnSrcGlobal>), grid, dim3(64 * (KS_)), 0, stream,   \
+                       src, out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);                         \
   }
 #define LC_ATTN_F32_KS(DT_)                                                                                         \
   switch (ks) {                                                                                                     \
@@ -785,6 +893,55 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
   }
 #undef LC_ATTN_F32_KS
 #undef LC_ATTN_F32
+  return hipGetLastError();
+}
+
+hipError_t convAttentionF32(const float* x, const float* w, const float* bias, int batch, int cin, int h, int wd,
+                            int cout, int kh, int kw, int sh, int sw, int ph, int pw, int S, int D, float* out,
+                            hipStream_t stream) {
+  const int oh = (h + 2 * ph - kh) / sh + 1;
+  const int ow = (wd + 2 * pw - kw) / sw + 1;
+  const long long n = static_cast<long long>(batch) * cout * oh * ow;
+  if (D <= 0 || D > 256 || S <= 0 || n <= 0 || n > AttnSrcConvRepeat::kOut ||
+      3LL * S * D >= (1LL << 31)) {
+    return hipErrorInvalidValue;
+  }
+  const long long xs = static_cast<long long>(batch) * cin * h * wd;
+  const long long ws = static_cast<long long>(cout) * cin * kh * kw;
+  const int big = 1 << 30;  // sizes beyond LDS staging just disable it
+  AttnSrcConvRepeat src{x, w, bias, cin, h, wd, cout, kh, kw, sh, sw, ph, pw, oh, ow, static_cast<int>(n),
+                        static_cast<int>(xs < big ? xs : big), static_cast<int>(ws < big ? ws : big),
+                        static_cast<size_t>(S) * D};
+  const float scale = 1.0f / sqrtf(static_cast<float>(D));
+  const int nqb = (S + 31) / 32;
+  const dim3 grid(nqb, 1);
+  const int dt = (D + 31) / 32;
+  // Key splits as for attentionF32, within LDS next to the 48 KB conv buffer.
+  int ks = 1;
+  while (ks < 4 && nqb * ks * 2 <= 512 && ks * 2 <= nqb && (ks * 2) * dt <= 8) {
+    ks *= 2;
+  }
+#define LC_CA_F32(DT_, KS_)                                                                                         \
+  hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false, AttnSrcConvRepeat>), grid, dim3(64 * (KS_)), 0, stream, \
+                     src, out, nullptr, S, D, 0, scale, 1.0f, 0.0f, 0)
+#define LC_CA_F32_KS(DT_)                                                                                           \
+  switch (ks) {                                                                                                     \
+    case 4: LC_CA_F32(DT_, (DT_ <= 2 ? 4 : 1)); break;                                                              \
+    case 2: LC_CA_F32(DT_, (DT_ <= 4 ? 2 : 1)); break;                                                              \
+    default: LC_CA_F32(DT_, 1); break;                                                                              \
+  }
+  switch (dt) {
+    case 1: LC_CA_F32_KS(1); break;
+    case 2: LC_CA_F32_KS(2); break;
+    case 3: LC_CA_F32_KS(3); break;
+    case 4: LC_CA_F32_KS(4); break;
+    case 5: LC_CA_F32(5, 1); break;
+    case 6: LC_CA_F32(6, 1); break;
+    case 7: LC_CA_F32(7, 1); break;
+    default: LC_CA_F32(8, 1); break;
+  }
+#undef LC_CA_F32_KS
+#undef LC_CA_F32
   return hipGetLastError();
 }
 

@@ -97,11 +97,30 @@ class DeviceBuffer {
 // the library uses, and one mutex that serialises host-side use of shared
 // buffers (the reference serialises its attention backend the same way,
 // src/attention_metal.mm:1855).
+// Pinned (page-locked) host staging that grows and never shrinks; allocated
+// with hipHostMalloc.  Small calls pack their host operands into it so that
+// one DMA copy replaces several pageable ones.
+class PinnedBuffer {
+ public:
+  PinnedBuffer() = default;
+  PinnedBuffer(const PinnedBuffer&) = delete;
+  PinnedBuffer& operator=(const PinnedBuffer&) = delete;
+  ~PinnedBuffer() { reset(); }
+  Status ensure(std::size_t bytes);
+  void reset();
+  void* get() const { return ptr_; }
+
+ private:
+  void* ptr_ = nullptr;
+  std::size_t bytes_ = 0;
+};
+
 struct HipContext {
   std::recursive_mutex mu;
   int device = 0;
   hipStream_t stream = nullptr;
   hipDeviceProp_t props{};
+  PinnedBuffer pinned;
   // Stream-K workspace of the fp32 GEMM (partial tiles + ready flags), one
   // slot per workgroup; used by launches on `stream` only, so never shared
   // by two kernels at once.

@@ -206,6 +206,30 @@ void DeviceBuffer::reset() {
   bytes_ = 0;
 }
 
+Status PinnedBuffer::ensure(std::size_t bytes) {
+  if (bytes <= bytes_ && ptr_ != nullptr) {
+    return Status::kSuccess;
+  }
+  const std::size_t want = std::max(bytes, bytes_ + bytes_ / 2);
+  reset();
+  void* p = nullptr;
+  const hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+  if (e != hipSuccess) {
+    return failHip(e, "hipHostMalloc");
+  }
+  ptr_ = p;
+  bytes_ = want;
+  return Status::kSuccess;
+}
+
+void PinnedBuffer::reset() {
+  if (ptr_ != nullptr) {
+    (void)hipHostFree(ptr_);  // synchronises the device: no copy can still use it
+  }
+  ptr_ = nullptr;
+  bytes_ = 0;
+}
+
 Status upload(HipContext* ctx, void* dst, const void* src, std::size_t bytes) {
   LC_HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
   return Status::kSuccess;

@@ -49,6 +49,28 @@ def test_conv_extra(lc, oracle, xs, ws, stride, pad):
         assert_parity(oracle.conv2d(x, w, bias, stride, pad, relu), got, "f32", f"conv {xs} {ws} relu={relu}")
 
 
+# The reference's own conv -> attention hotspot shapes (README.md Pipeline
+# Bench: conv n=1 c=3->16 h=w=8 k=3 (pad 1) + attention seq 48/96/192, d
+# 48/8), served by the fused one-launch kernel, plus shapes whose conv output
+# exceeds the fused kernel's 8192 values (the im2col + GEMM + repeat chain)
+# and a strided / unpadded one.
+@pytest.mark.parametrize("xs,ws,stride,pad,seq,hd", [
+    ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 48, 48),
+    ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 192, 48),
+    ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 192, 8),
+    ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 96, 48),
+    ((2, 3, 33, 31), (16, 3, 3, 3), (1, 1), (1, 1), 100, 64),
+    ((1, 4, 40, 40), (24, 4, 3, 3), (1, 1), (1, 1), 64, 200),
+    ((1, 2, 9, 11), (5, 2, 3, 2), (2, 1), (0, 0), 30, 7),
+])
+def test_conv_attention_shapes(lc, oracle, xs, ws, stride, pad, seq, hd):
+    x, w = synth.normal(xs, stream=40), synth.normal(ws, std=0.3, stream=41)
+    bias = synth.normal((ws[0],), stream=42)
+    got = lc.api.conv_attention_torchstrong_nchw(x, w, bias, seq, hd, stride[0], stride[1], pad[0], pad[1])
+    ref = oracle.conv_attention(x, w, bias, seq, hd, stride, pad)
+    assert_parity(ref.ravel(), got, "f32", f"conv_attention {xs} {ws} seq={seq} d={hd}")
+
+
 def test_conv_attention_graph_mode_matches_eager(lc):
     x, w = synth.normal((1, 3, 8, 8), stream=4), synth.normal((8, 3, 3, 3), stream=5)
     e = lc.api.conv_attention_torchstrong_nchw(x, w, None, 16, 16, 1, 1, 1, 1, execution_mode="eager")
