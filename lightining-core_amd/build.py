@@ -10,6 +10,7 @@ import concurrent.futures
 import glob
 import os
 import subprocess
+import sysconfig
 import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -47,7 +48,24 @@ def _compile(src: str) -> str:
     return obj
 
 
+ADDR_SRC = os.path.join(CSRC, "pyaddr.c")
+ADDR_LIB = os.path.join(HERE, "lightning_core", "_addr.so")
+
+
+def build_addr() -> str:
+    """The binding's buffer-address helper (a CPython extension, host only)."""
+    inc = sysconfig.get_paths()["include"]
+    tmp = ADDR_LIB + ".tmp"
+    cmd = ["gcc", "-O2", "-shared", "-fPIC", "-I" + inc, ADDR_SRC, "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("pyaddr build failed\n" + r.stdout + r.stderr)
+    os.replace(tmp, ADDR_LIB)
+    return ADDR_LIB
+
+
 def build(jobs: int | None = None) -> str:
+    build_addr()
     os.makedirs(BUILD, exist_ok=True)
     jobs = jobs or min(8, os.cpu_count() or 4)
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as ex:

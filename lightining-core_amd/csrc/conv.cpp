@@ -15,6 +15,7 @@
 //    [B*T, E]; QKV GEMM writing head-major Q/K and transposed V; flash
 //    attention writing heads concatenated [B*T, E]; output projection.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
@@ -252,16 +253,26 @@ lcError_t lcConvAttentionTorchstrongNchw(const float* x, const float* w, const f
   if (g.outSize() <= 8192 && 3 * need < (std::size_t{1} << 31)) {
     // The reference's hotspot shapes (small conv, repeated into Q/K/V): one
     // fused launch, conv recomputed per workgroup into LDS.
-    // x, w and bias go over in one DMA copy from pinned staging (these calls
-    // are small enough that per-copy overhead is most of their time), and
-    // the output comes back the same way.
+    // These calls are small enough that per-copy overhead is most of their
+    // time.  x, w and bias are packed into pinned staging.  When the kernel
+    // stages them in LDS (it then reads each value once per workgroup) it
+    // reads them, and writes the output, through the staging's device alias:
+    // no copy at all.  Otherwise the inputs go over in one DMA copy and the
+    // output comes back the same way.
+    const int ib = static_cast<int>(g.batch), ic = static_cast<int>(g.in_c), ih = static_cast<int>(g.in_h),
+              iw = static_cast<int>(g.in_w), oc = static_cast<int>(g.out_c), kh = static_cast<int>(g.kh),
+              kw = static_cast<int>(g.kw), sh = static_cast<int>(g.sh), sw = static_cast<int>(g.sw),
+              ph = static_cast<int>(g.ph), pw = static_cast<int>(g.pw);
+    static const bool force_copy = std::getenv("LC_CONV_ATTN_COPY") != nullptr;
+    const bool mapped = !force_copy && kern::convAttentionStagesInputs(ib, ic, ih, iw, oc, kh, kw, sh, sw, ph, pw);
     const std::size_t xs = g.batch * g.in_c * g.in_h * g.in_w;
     const std::size_t ws = g.out_c * g.kin();
     const std::size_t bs = bias != nullptr ? g.out_c : 0;
     const std::size_t in_floats = xs + ws + bs;
-    st = r.x.ensure(in_floats * sizeof(float));
-    if (st == Status::kSuccess) st = r.attn_out.ensure(need * sizeof(float));
-    if (st == Status::kSuccess) st = ctx->pinned.ensure(std::max(in_floats, need) * sizeof(float));
+    const std::size_t out_at = mapped ? roundUp(in_floats, 64) : 0;  // 256-byte aligned output
+    st = ctx->pinned.ensure(std::max(in_floats, out_at + need) * sizeof(float));
+    if (st == Status::kSuccess && !mapped) st = r.x.ensure(in_floats * sizeof(float));
+    if (st == Status::kSuccess && !mapped) st = r.attn_out.ensure(need * sizeof(float));
     if (st != Status::kSuccess) {
       return toLc(st);
     }
@@ -271,30 +282,37 @@ lcError_t lcConvAttentionTorchstrongNchw(const float* x, const float* w, const f
     if (bs != 0) {
       std::memcpy(stage + xs + ws, bias, bs * sizeof(float));
     }
-    st = upload(ctx, r.x.get(), stage, in_floats * sizeof(float));
-    if (st != Status::kSuccess) {
-      return toLc(st);
+    const float* dx = nullptr;
+    float* dout = nullptr;
+    if (mapped) {
+      dx = static_cast<const float*>(ctx->pinned.device());
+      dout = static_cast<float*>(ctx->pinned.device()) + out_at;
+    } else {
+      st = upload(ctx, r.x.get(), stage, in_floats * sizeof(float));
+      if (st != Status::kSuccess) {
+        return toLc(st);
+      }
+      dx = r.x.as<float>();
+      dout = r.attn_out.as<float>();
     }
-    const float* dx = r.x.as<float>();
     const float* dw = dx + xs;
     const float* dbias = bs != 0 ? dx + xs + ws : nullptr;
     traceOpDispatch(TraceOp::kConv2dNchw, Device::kHIP, Device::kHIP, false, g.rows() * g.out_c * g.kin());
     traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, seq_len * seq_len * head_dim);
-    const hipError_t e = kern::convAttentionF32(
-        dx, dw, dbias, static_cast<int>(g.batch), static_cast<int>(g.in_c),
-        static_cast<int>(g.in_h), static_cast<int>(g.in_w), static_cast<int>(g.out_c), static_cast<int>(g.kh),
-        static_cast<int>(g.kw), static_cast<int>(g.sh), static_cast<int>(g.sw), static_cast<int>(g.ph),
-        static_cast<int>(g.pw), static_cast<int>(seq_len), static_cast<int>(head_dim), r.attn_out.as<float>(),
-        ctx->stream);
+    const hipError_t e = kern::convAttentionF32(dx, dw, dbias, ib, ic, ih, iw, oc, kh, kw, sh, sw, ph, pw,
+                                                static_cast<int>(seq_len), static_cast<int>(head_dim), dout,
+                                                ctx->stream);
     if (e != hipSuccess) {
       return toLc(failHip(e, "conv_attention launch"));
     }
-    st = download(ctx, stage, r.attn_out.get(), need * sizeof(float));
+    if (!mapped) {
+      st = download(ctx, stage, r.attn_out.get(), need * sizeof(float));
+    }
     if (st == Status::kSuccess) {
       st = syncStream(ctx);
     }
     if (st == Status::kSuccess) {
-      std::memcpy(out, stage, need * sizeof(float));
+      std::memcpy(out, stage + out_at, need * sizeof(float));
     }
     return toLc(st);
   }

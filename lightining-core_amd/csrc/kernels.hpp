@@ -68,6 +68,10 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
 hipError_t convAttentionF32(const float* x, const float* w, const float* bias, int batch, int cin, int h, int wd,
                             int cout, int kh, int kw, int sh, int sw, int ph, int pw, int S, int D, float* out,
                             hipStream_t stream);
+// True when convAttentionF32 reads x, w and bias exactly once per workgroup
+// (all staged in LDS): then they may live in mapped host memory.
+bool convAttentionStagesInputs(int batch, int cin, int h, int wd, int cout, int kh, int kw, int sh, int sw, int ph,
+                               int pw);
 // Train step backward: v -= lr * P^T . (2 (out - target) / (S*D)) per head,
 // P recomputed from q, k and the forward's stats.
 hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const float* out, const float* target,

@@ -42,10 +42,16 @@ struct AttnSrcGlobal {
   const float* v;
   static constexpr int kLds = 0;
   static constexpr bool kVec = true;
+  static constexpr bool kClamp = false;  // padding cells are not loaded
+  // A position is the flat element index; W selects Q (0), K (1) or V (2).
+  using Pos = size_t;
   __device__ void prologue(float*, int) const {}
-  __device__ float ldq(const float*, size_t i) const { return q[i]; }
-  __device__ float ldk(const float*, size_t i) const { return k[i]; }
-  __device__ float ldv(const float*, size_t i) const { return v[i]; }
+  template <int W>
+  __device__ Pos at(size_t i) const { return i; }
+  __device__ size_t delta(size_t d) const { return d; }
+  __device__ Pos fwd(Pos p, size_t d) const { return p + d; }
+  template <int W>
+  __device__ float ld(const float*, Pos p) const { return (W == 0 ? q : W == 1 ? k : v)[p]; }
 };
 
 // The reference's conv -> attention chain (bind_integrated.cpp:614-730):
@@ -66,50 +72,58 @@ struct AttnSrcConvRepeat {
   static constexpr int kOut = 8192;
   static constexpr int kLds = 12288;
   static constexpr bool kVec = false;
+  static constexpr bool kClamp = true;  // every position is in bounds: padding loads a real value
+  // Positions are indices into the conv output (< n): element i of Q, K, V
+  // is conv[(W * S * D + i) mod n].  A fill walks its tile with pre-reduced
+  // strides (one conditional subtract per step instead of a division).
+  using Pos = uint32_t;
   __device__ void prologue(float* buf, int nthreads) const {
-    // x and w are staged behind the output when they fit (one coalesced pass
-    // instead of a dependent global load per multiply-add).
-    const bool staged = n + xs + ws <= kLds;
-    const float* xp = x;
-    const float* wp = w;
-    if (staged) {
+    // x, w and bias are staged behind the output when they fit (one
+    // coalesced pass, then LDS reads instead of dependent global loads per
+    // multiply-add).
+    if (staged()) {
       float* xb = buf + n;
       float* wb = xb + xs;
+      float* bb = wb + ws;
       for (int i = threadIdx.x; i < xs; i += nthreads) {
         xb[i] = x[i];
       }
       for (int i = threadIdx.x; i < ws; i += nthreads) {
         wb[i] = w[i];
       }
+      if (bias != nullptr) {
+        for (int i = threadIdx.x; i < cout; i += nthreads) {
+          bb[i] = bias[i];
+        }
+      }
       __syncthreads();
-      xp = xb;
-      wp = wb;
+      conv(buf, xb, wb, bias != nullptr ? bb : nullptr, nthreads);
+    } else {
+      conv(buf, x, w, bias, nthreads);
+    }
+    __syncthreads();
+  }
+  // x, w and bias all fit in LDS next to the output: the only case in which
+  // they are read from global memory once per workgroup (the host may then
+  // hand over mapped host memory).
+  __host__ __device__ bool staged() const { return n + xs + ws + cout <= kLds; }
+  __device__ void conv(float* buf, const float* xp, const float* wp, const float* bp, int nthreads) const {
+    const int hw = oh * ow;
+    if (kh == 3 && kw == 3 && cin <= 4) {
+      conv3x3(buf, xp, wp, bp, nthreads);
+      return;
     }
     for (int f = threadIdx.x; f < n; f += nthreads) {
-      const int ox = f % ow;
-      int t = f / ow;
-      const int oy = t % oh;
-      t /= oh;
+      const int t = f / hw;
+      const int pix = f - t * hw;
+      const int oy = pix / ow;
+      const int ox = pix - oy * ow;
       const int oc = t % cout;
       const int b = t / cout;
       float acc = 0.0f;
       for (int c = 0; c < cin; ++c) {
         const float* xc = xp + (static_cast<size_t>(b) * cin + c) * h * wd;
         const float* wc = wp + (static_cast<size_t>(oc) * cin + c) * kh * kw;
-        if (kh == 3 && kw == 3) {
-          // the hotspot kernel size: all nine loads issued together
-#pragma unroll
-          for (int ky = 0; ky < 3; ++ky) {
-            const int iy = oy * sh + ky - ph;
-#pragma unroll
-            for (int kx = 0; kx < 3; ++kx) {
-              const int ix = ox * sw + kx - pw;
-              const float xv = (iy >= 0 && iy < h && ix >= 0 && ix < wd) ? xc[iy * wd + ix] : 0.0f;
-              acc += xv * wc[ky * 3 + kx];
-            }
-          }
-          continue;
-        }
         for (int ky = 0; ky < kh; ++ky) {
           const int iy = oy * sh + ky - ph;
           for (int kx = 0; kx < kw; ++kx) {
@@ -119,24 +133,142 @@ struct AttnSrcConvRepeat {
           }
         }
       }
-      if (bias != nullptr) {
-        acc += bias[oc];
+      if (bp != nullptr) {
+        acc += bp[oc];
       }
       buf[f] = acc > 0.0f ? acc : 0.0f;
     }
-    __syncthreads();
+  }
+  // 3x3 kernels with at most 4 input channels (the hotspot shapes): one
+  // thread per (output pixel, group of output channels).  The pixel's cin*9
+  // inputs are loaded once (clamped in-bounds loads, zeroed outside the
+  // image) and reused for every channel of the group; a wave's pixels share
+  // their channel, so each weight read is one LDS broadcast.  Same
+  // accumulation order as the general loop: (c, ky, kx), bias last.
+  __device__ void conv3x3(float* buf, const float* xp, const float* wp, const float* bp, int nthreads) const {
+    const int hw = oh * ow;
+    const int npix = n / cout;  // batch * oh * ow
+    int groups = nthreads / npix;
+    groups = groups < 1 ? 1 : (groups > cout ? cout : groups);
+    const int ocb = (cout + groups - 1) / groups;
+    for (int item = threadIdx.x; item < npix * groups; item += nthreads) {
+      const int g = item / npix;
+      const int pix = item - g * npix;
+      const int b = pix / hw;
+      const int rem = pix - b * hw;
+      const int oy = rem / ow;
+      const int ox = rem - oy * ow;
+      float xv[36];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if (c < cin) {
+          const float* xc = xp + (static_cast<size_t>(b) * cin + c) * h * wd;
+#pragma unroll
+          for (int ky = 0; ky < 3; ++ky) {
+            const int iy = oy * sh + ky - ph;
+            const int iyc = min(max(iy, 0), h - 1);
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+              const int ix = ox * sw + kx - pw;
+              const int ixc = min(max(ix, 0), wd - 1);
+              const float v = xc[iyc * wd + ixc];
+              xv[c * 9 + ky * 3 + kx] = (iy == iyc && ix == ixc) ? v : 0.0f;
+            }
+          }
+        }
+      }
+      const int oc_end = min(cout, (g + 1) * ocb);
+      float* dst = buf + static_cast<size_t>(b) * cout * hw + rem;
+      for (int oc = g * ocb; oc < oc_end; ++oc) {
+        const float* wc = wp + oc * cin * 9;
+        float acc = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if (c < cin) {
+#pragma unroll
+            for (int e = 0; e < 9; ++e) {
+              acc += xv[c * 9 + e] * wc[c * 9 + e];
+            }
+          }
+        }
+        if (bp != nullptr) {
+          acc += bp[oc];
+        }
+        dst[oc * hw] = acc > 0.0f ? acc : 0.0f;
+      }
+    }
   }
   // 32-bit index arithmetic (the host keeps 3*S*D below 2^31).
-  __device__ float ldq(const float* buf, size_t i) const {
-    return buf[static_cast<uint32_t>(i) % static_cast<uint32_t>(n)];
+  template <int W>
+  __device__ Pos at(size_t i) const {
+    return static_cast<uint32_t>(W * need + i) % static_cast<uint32_t>(n);
   }
-  __device__ float ldk(const float* buf, size_t i) const {
-    return buf[static_cast<uint32_t>(need + i) % static_cast<uint32_t>(n)];
+  __device__ uint32_t delta(size_t d) const { return static_cast<uint32_t>(d % static_cast<size_t>(n)); }
+  __device__ Pos fwd(Pos p, uint32_t d) const {
+    p += d;
+    return p >= static_cast<uint32_t>(n) ? p - static_cast<uint32_t>(n) : p;
   }
-  __device__ float ldv(const float* buf, size_t i) const {
-    return buf[static_cast<uint32_t>(2 * need + i) % static_cast<uint32_t>(n)];
-  }
+  template <int W>
+  __device__ float ld(const float* buf, Pos p) const { return buf[p]; }
 };
+
+// Fills rows row0, row0 + rstep, ... (< 32) of 32 x DP tiles (row stride
+// ldd) with operands W0 (and W1 when NT = 2) of rows first + r of one head;
+// rows >= S and columns >= D are zero.  Lane l covers column l (and l + 64,
+// ...) of a row, or for DP = 32 a column of one of two adjacent rows.  The
+// operands share positions: their loads are issued together.
+template <int DP, int NT, int W0, int W1, typename Src>
+__device__ inline void fill_rows(const Src& src, const float* buf, float* dst0, int ldd0, float* dst1, int ldd1,
+                                 int row0, int rstep, int first, int S, int D, size_t head, int lane) {
+  constexpr int RPI = DP >= 64 ? 1 : 64 / DP;
+  constexpr int CPR = DP >= 64 ? (DP + 63) / 64 : 1;
+  const int lr = DP >= 64 ? 0 : lane / DP;
+  const int lc = DP >= 64 ? lane : lane % DP;
+  const int rstride = rstep * RPI;
+  const int r0 = row0 * RPI + lr;
+  const size_t flat = head + static_cast<size_t>(first + r0) * D + lc;
+  auto p0 = src.template at<W0>(flat);
+  auto p1 = src.template at<W1>(flat);
+  // kClamp: padding cells load element 0 of the head (always in bounds) and
+  // store zero, so every load is unconditional and the unrolled rows' loads
+  // overlap instead of each sitting in its own exec-masked block.
+  const auto z0 = src.template at<W0>(head);
+  const auto z1 = src.template at<W1>(head);
+  const auto drow = src.delta(static_cast<size_t>(rstride) * D);
+  decltype(src.delta(0)) dch[CPR];
+#pragma unroll
+  for (int ch = 0; ch < CPR; ++ch) {
+    dch[ch] = src.delta(static_cast<size_t>(64 * ch));
+  }
+#pragma unroll 8
+  for (int r = r0; r < 32; r += rstride) {
+    const bool rok = first + r < S;
+#pragma unroll
+    for (int ch = 0; ch < CPR; ++ch) {
+      const int c = lc + 64 * ch;
+      if (c < DP) {
+        const bool ok = rok && c < D;
+        if constexpr (Src::kClamp) {
+          const float v0 = src.template ld<W0>(buf, ok ? (ch == 0 ? p0 : src.fwd(p0, dch[ch])) : z0);
+          dst0[r * ldd0 + c] = ok ? v0 : 0.0f;
+          if constexpr (NT == 2) {
+            const float v1 = src.template ld<W1>(buf, ok ? (ch == 0 ? p1 : src.fwd(p1, dch[ch])) : z1);
+            dst1[r * ldd1 + c] = ok ? v1 : 0.0f;
+          }
+        } else {
+          dst0[r * ldd0 + c] = ok ? src.template ld<W0>(buf, ch == 0 ? p0 : src.fwd(p0, dch[ch])) : 0.0f;
+          if constexpr (NT == 2) {
+            dst1[r * ldd1 + c] = ok ? src.template ld<W1>(buf, ch == 0 ? p1 : src.fwd(p1, dch[ch])) : 0.0f;
+          }
+        }
+      }
+    }
+    p0 = src.fwd(p0, drow);
+    if constexpr (NT == 2) {
+      p1 = src.fwd(p1, drow);
+    }
+  }
+}
 
 template <int DT, int KS, bool VEC, typename Src>
 __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* __restrict__ out,
@@ -160,11 +292,7 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
   out += head;
   src.prologue(srcbuf, 64 * KS);
 
-  for (int idx = threadIdx.x; idx < 32 * DP; idx += 64 * KS) {
-    const int r = idx / DP;
-    const int c = idx - r * DP;
-    Qs[r][c] = (q0 + r < S && c < D) ? src.ldq(srcbuf, head + static_cast<size_t>(q0 + r) * D + c) : 0.0f;
-  }
+  fill_rows<DP, 1, 0, 0>(src, srcbuf, &Qs[0][0], DP + 1, nullptr, 0, wave, KS, q0, S, D, head, lane);
   __syncthreads();
 
   floatx16 o[DT];
@@ -220,15 +348,7 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
         fetch(j0 + 32 * KS);
       }
     } else {
-#pragma unroll 8
-      for (int idx = lane; idx < 32 * DP; idx += 64) {
-        const int r = idx / DP;
-        const int cc = idx - r * DP;
-        const bool ok = (j0 + r < S && cc < D);
-        const size_t off = head + static_cast<size_t>(j0 + r) * D + cc;
-        Ks[r][cc] = ok ? src.ldk(srcbuf, off) : 0.0f;
-        Vs[r][cc] = ok ? src.ldv(srcbuf, off) : 0.0f;
-      }
+      fill_rows<DP, 2, 1, 2>(src, srcbuf, &Ks[0][0], DP + 1, &Vs[0][0], DP, 0, 1, j0, S, D, head, lane);
     }
     __builtin_amdgcn_wave_barrier();
 
@@ -344,23 +464,40 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
     stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2] = m_fin;
     stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2 + 1] = l_fin;
   }
-  if (qi < S) {
+  // The 32 x D output block goes through Qs (free: every wave is past its
+  // QK^T) so that the stores cover contiguous rows: full lines in HBM, and
+  // few large transactions when out is mapped host memory.
 #pragma unroll
-    for (int t = 0; t < DT; ++t) {
+  for (int t = 0; t < DT; ++t) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int d = t * 32 + acc_row(i, lane);
-        if (d < D) {
-          float val = o[t][i] * inv;
-          if (post_scale != 1.0f || post_bias != 0.0f || post_relu) {
-            val = val * post_scale + post_bias;
-            if (post_relu && val < 0.0f) {
-              val = 0.0f;
-            }
+    for (int i = 0; i < 16; ++i) {
+      const int d = t * 32 + acc_row(i, lane);
+      if (d < D) {
+        float val = o[t][i] * inv;
+        if (post_scale != 1.0f || post_bias != 0.0f || post_relu) {
+          val = val * post_scale + post_bias;
+          if (post_relu && val < 0.0f) {
+            val = 0.0f;
           }
-          out[static_cast<size_t>(qi) * D + d] = val;
         }
+        Qs[lane & 31][d] = val;
       }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();
+  const int total = min(32, S - q0) * D;
+  const int qstep = 64 / D;
+  const int cstep = 64 - qstep * D;
+  int r = lane / D;
+  int c = lane - r * D;
+  float* dst = out + static_cast<size_t>(q0) * D;
+  for (int idx = lane; idx < total; idx += 64) {
+    dst[idx] = Qs[r][c];
+    r += qstep;
+    c += cstep;
+    if (c >= D) {
+      c -= D;
+      ++r;
     }
   }
 }
@@ -894,6 +1031,16 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
 #undef LC_ATTN_F32_KS
 #undef LC_ATTN_F32
   return hipGetLastError();
+}
+
+bool convAttentionStagesInputs(int batch, int cin, int h, int wd, int cout, int kh, int kw, int sh, int sw, int ph,
+                               int pw) {
+  const int oh = (h + 2 * ph - kh) / sh + 1;
+  const int ow = (wd + 2 * pw - kw) / sw + 1;
+  const long long n = static_cast<long long>(batch) * cout * oh * ow;
+  const long long xs = static_cast<long long>(batch) * cin * h * wd;
+  const long long ws = static_cast<long long>(cout) * cin * kh * kw;
+  return n + xs + ws + cout <= AttnSrcConvRepeat::kLds;
 }
 
 hipError_t convAttentionF32(const float* x, const float* w, const float* bias, int batch, int cin, int h, int wd,

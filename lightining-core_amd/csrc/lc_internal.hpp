@@ -98,8 +98,9 @@ class DeviceBuffer {
 // buffers (the reference serialises its attention backend the same way,
 // src/attention_metal.mm:1855).
 // Pinned (page-locked) host staging that grows and never shrinks; allocated
-// with hipHostMalloc.  Small calls pack their host operands into it so that
-// one DMA copy replaces several pageable ones.
+// with hipHostMalloc, which also maps it into the device address space.
+// Small calls pack their host operands into it so that one DMA copy replaces
+// several pageable ones, or hand its device alias straight to a kernel.
 class PinnedBuffer {
  public:
   PinnedBuffer() = default;
@@ -109,9 +110,13 @@ class PinnedBuffer {
   Status ensure(std::size_t bytes);
   void reset();
   void* get() const { return ptr_; }
+  // The same bytes as seen by kernels (host writes are visible to a kernel
+  // launched after them; kernel writes are visible after a stream sync).
+  void* device() const { return dev_; }
 
  private:
   void* ptr_ = nullptr;
+  void* dev_ = nullptr;
   std::size_t bytes_ = 0;
 };
 

@@ -213,11 +213,18 @@ Status PinnedBuffer::ensure(std::size_t bytes) {
   const std::size_t want = std::max(bytes, bytes_ + bytes_ / 2);
   reset();
   void* p = nullptr;
-  const hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
+  hipError_t e = hipHostMalloc(&p, want, hipHostMallocDefault);
   if (e != hipSuccess) {
     return failHip(e, "hipHostMalloc");
   }
+  void* d = nullptr;
+  e = hipHostGetDevicePointer(&d, p, 0);
+  if (e != hipSuccess) {
+    (void)hipHostFree(p);
+    return failHip(e, "hipHostGetDevicePointer");
+  }
   ptr_ = p;
+  dev_ = d;
   bytes_ = want;
   return Status::kSuccess;
 }
@@ -227,6 +234,7 @@ void PinnedBuffer::reset() {
     (void)hipHostFree(ptr_);  // synchronises the device: no copy can still use it
   }
   ptr_ = nullptr;
+  dev_ = nullptr;
   bytes_ = 0;
 }
 

@@ -67,8 +67,17 @@ def _f32(a) -> np.ndarray:
     return np.ascontiguousarray(a, dtype=np.float32)
 
 
+try:  # the compiled buffer-address helper, built next to the C library
+    from ._addr import addr as _addr
+except ImportError:  # not built: numpy's own (slower) route
+    _addr = None
+
+
 def _fp(a):
-    return None if a is None else a.ctypes.data_as(N.FP)
+    """Address of a C-contiguous array for a void* buffer parameter."""
+    if a is None:
+        return None
+    return _addr(a) if _addr is not None else a.ctypes.data
 
 
 def _require_2d(a: np.ndarray, name: str, what: str):

@@ -17,6 +17,9 @@ c_float = ctypes.c_float
 c_char_p = ctypes.c_char_p
 c_void_p = ctypes.c_void_p
 FP = ctypes.POINTER(ctypes.c_float)
+# Buffer parameters are declared void*: they take the plain addresses the
+# binding passes (see _core._fp) as well as ctypes pointers such as FP.
+BUF = ctypes.c_void_p
 
 # lcError_t
 LC_SUCCESS, LC_NOT_INITIALIZED, LC_INVALID_VALUE, LC_OUT_OF_MEMORY, LC_NOT_SUPPORTED, LC_DRIVER_ERROR, LC_UNKNOWN = range(7)
@@ -146,44 +149,44 @@ SIGNATURES = {
     "lcDecodeRuntimeTraceDispatchDetail": (c_int, [c_int, P(c_int), P(c_int), P(c_int)]),
     "lcAttentionIoPolicyDefault": (AttentionIoPolicyC, []),
     "lcAttentionImplementationName": (c_char_p, [c_int]),
-    "lcAttentionForward": (_E, [FP, FP, FP, FP, P(AttentionConfig), c_int]),
-    "lcAttentionForwardWithPolicy": (_E, [FP, FP, FP, FP, P(AttentionConfig), c_int, P(AttentionIoPolicyC)]),
-    "lcAttentionForwardBatched": (_E, [FP, FP, FP, FP, P(AttentionBatchedConfig), c_int, P(AttentionIoPolicyC)]),
+    "lcAttentionForward": (_E, [BUF, BUF, BUF, BUF, P(AttentionConfig), c_int]),
+    "lcAttentionForwardWithPolicy": (_E, [BUF, BUF, BUF, BUF, P(AttentionConfig), c_int, P(AttentionIoPolicyC)]),
+    "lcAttentionForwardBatched": (_E, [BUF, BUF, BUF, BUF, P(AttentionBatchedConfig), c_int, P(AttentionIoPolicyC)]),
     "lcAttentionSessionCreate": (_E, [P(AttentionConfig), c_int, P(c_void_p)]),
     "lcAttentionSessionCreateBatched": (_E, [P(AttentionBatchedConfig), c_int, P(c_void_p)]),
     "lcAttentionSessionDestroy": (_E, [c_void_p]),
     "lcAttentionSessionSetDefaultPolicy": (_E, [c_void_p, P(AttentionIoPolicyC)]),
     "lcAttentionSessionGetDefaultPolicy": (_E, [c_void_p, P(AttentionIoPolicyC)]),
-    "lcAttentionSessionForward": (_E, [c_void_p, FP, FP, FP, FP]),
-    "lcAttentionSessionForwardWithPolicy": (_E, [c_void_p, FP, FP, FP, FP, P(AttentionIoPolicyC)]),
+    "lcAttentionSessionForward": (_E, [c_void_p, BUF, BUF, BUF, BUF]),
+    "lcAttentionSessionForwardWithPolicy": (_E, [c_void_p, BUF, BUF, BUF, BUF, P(AttentionIoPolicyC)]),
     "lcAttentionSessionRunCached": (_E, [c_void_p, c_size]),
-    "lcAttentionTrainStep": (_E, [FP, FP, FP, FP, FP, c_float, P(AttentionConfig), c_int, FP]),
-    "lcAttentionTrainStepWithPolicy": (_E, [FP, FP, FP, FP, FP, c_float, P(AttentionConfig), c_int, FP,
+    "lcAttentionTrainStep": (_E, [BUF, BUF, BUF, BUF, BUF, c_float, P(AttentionConfig), c_int, BUF]),
+    "lcAttentionTrainStepWithPolicy": (_E, [BUF, BUF, BUF, BUF, BUF, c_float, P(AttentionConfig), c_int, BUF,
                                             P(AttentionIoPolicyC)]),
-    "lcAttentionSessionTrainStep": (_E, [c_void_p, FP, FP, FP, FP, FP, c_float, FP]),
-    "lcAttentionSessionTrainStepWithPolicy": (_E, [c_void_p, FP, FP, FP, FP, FP, c_float, FP, P(AttentionIoPolicyC)]),
+    "lcAttentionSessionTrainStep": (_E, [c_void_p, BUF, BUF, BUF, BUF, BUF, c_float, BUF]),
+    "lcAttentionSessionTrainStepWithPolicy": (_E, [c_void_p, BUF, BUF, BUF, BUF, BUF, c_float, BUF, P(AttentionIoPolicyC)]),
     "lcMatMulIoPolicyDefault": (MatMulIoPolicyC, []),
-    "lcMatMul": (_E, [FP, FP, FP, c_size, c_size, c_size, c_int]),
-    "lcMatMulWithPolicy": (_E, [FP, FP, FP, c_size, c_size, c_size, c_int, P(MatMulIoPolicyC)]),
-    "lcMatMulWithPolicyBatched": (_E, [FP, FP, FP, c_size, c_size, c_size, c_int, P(MatMulIoPolicyC), c_size]),
+    "lcMatMul": (_E, [BUF, BUF, BUF, c_size, c_size, c_size, c_int]),
+    "lcMatMulWithPolicy": (_E, [BUF, BUF, BUF, c_size, c_size, c_size, c_int, P(MatMulIoPolicyC)]),
+    "lcMatMulWithPolicyBatched": (_E, [BUF, BUF, BUF, c_size, c_size, c_size, c_int, P(MatMulIoPolicyC), c_size]),
     "lcMatMulResetTuning": (_E, []),
     "lcMatMulResidentSessionCreate": (_E, [c_size, c_size, c_size, c_int, P(c_void_p)]),
     "lcMatMulResidentSessionDestroy": (_E, [c_void_p]),
-    "lcMatMulResidentSessionStart": (_E, [c_void_p, FP, FP, FP]),
-    "lcMatMulResidentSessionRun": (_E, [c_void_p, FP, FP, FP]),
-    "lcMatMulResidentSessionFinish": (_E, [c_void_p, FP, FP, FP]),
-    "lcMatMulResidentSessionSync": (_E, [c_void_p, FP, FP, FP]),
-    "lcMatMulResidentSessionRunBatchSync": (_E, [c_void_p, FP, FP, FP, c_size]),
-    "lcMatMulResidentSessionRunBatchSyncNoDownload": (_E, [c_void_p, FP, FP, FP, c_size]),
+    "lcMatMulResidentSessionStart": (_E, [c_void_p, BUF, BUF, BUF]),
+    "lcMatMulResidentSessionRun": (_E, [c_void_p, BUF, BUF, BUF]),
+    "lcMatMulResidentSessionFinish": (_E, [c_void_p, BUF, BUF, BUF]),
+    "lcMatMulResidentSessionSync": (_E, [c_void_p, BUF, BUF, BUF]),
+    "lcMatMulResidentSessionRunBatchSync": (_E, [c_void_p, BUF, BUF, BUF, c_size]),
+    "lcMatMulResidentSessionRunBatchSyncNoDownload": (_E, [c_void_p, BUF, BUF, BUF, c_size]),
     "lcMatMulResidentSessionRunBatchSyncCachedNoDownload": (_E, [c_void_p, c_size]),
-    "lcConv2dNchw": (_E, [FP, FP, FP, FP] + [c_size] * 11 + [c_int, c_int]),
-    "lcConvAttentionTorchstrongNchw": (_E, [FP, FP, FP, FP] + [c_size] * 13 + [c_int]),
+    "lcConv2dNchw": (_E, [BUF, BUF, BUF, BUF] + [c_size] * 11 + [c_int, c_int]),
+    "lcConvAttentionTorchstrongNchw": (_E, [BUF, BUF, BUF, BUF] + [c_size] * 13 + [c_int]),
     "lcVitBlockSessionCreate": (_E, [P(VitBlockConfig), c_int, P(c_void_p)]),
     "lcVitBlockSessionDestroy": (_E, [c_void_p]),
-    "lcVitBlockSessionSetWeights": (_E, [c_void_p, FP, FP, FP]),
-    "lcVitBlockSessionForward": (_E, [c_void_p, FP, FP]),
+    "lcVitBlockSessionSetWeights": (_E, [c_void_p, BUF, BUF, BUF]),
+    "lcVitBlockSessionForward": (_E, [c_void_p, BUF, BUF]),
     "lcVitBlockSessionRunCached": (_E, [c_void_p, c_size]),
-    "lcVitBlockForward": (_E, [FP, FP, FP, FP, FP, P(VitBlockConfig), c_int]),
+    "lcVitBlockForward": (_E, [BUF, BUF, BUF, BUF, BUF, P(VitBlockConfig), c_int]),
     "lcHipGetDeviceInfo": (_E, [P(HipDeviceInfo)]),
     "lcHipTimerCreate": (_E, [P(c_void_p)]),
     "lcHipTimerDestroy": (_E, [c_void_p]),

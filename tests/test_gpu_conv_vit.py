@@ -52,8 +52,11 @@ def test_conv_extra(lc, oracle, xs, ws, stride, pad):
 # The reference's own conv -> attention hotspot shapes (README.md Pipeline
 # Bench: conv n=1 c=3->16 h=w=8 k=3 (pad 1) + attention seq 48/96/192, d
 # 48/8), served by the fused one-launch kernel, plus shapes whose conv output
-# exceeds the fused kernel's 8192 values (the im2col + GEMM + repeat chain)
-# and a strided / unpadded one.
+# exceeds the fused kernel's 8192 values (the im2col + GEMM + repeat chain).
+# Fused variants: a strided / unpadded non-3x3 kernel, 3x3 with stride 2 and
+# batch 2 (pixel count not a multiple of 64), 4 input channels unpadded, an
+# input too large to stage in LDS (read from global memory), and 5 input
+# channels (the general conv loop).
 @pytest.mark.parametrize("xs,ws,stride,pad,seq,hd", [
     ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 48, 48),
     ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 192, 48),
@@ -62,6 +65,10 @@ def test_conv_extra(lc, oracle, xs, ws, stride, pad):
     ((2, 3, 33, 31), (16, 3, 3, 3), (1, 1), (1, 1), 100, 64),
     ((1, 4, 40, 40), (24, 4, 3, 3), (1, 1), (1, 1), 64, 200),
     ((1, 2, 9, 11), (5, 2, 3, 2), (2, 1), (0, 0), 30, 7),
+    ((2, 1, 15, 13), (6, 1, 3, 3), (2, 2), (1, 1), 40, 24),
+    ((1, 4, 12, 10), (7, 4, 3, 3), (1, 1), (0, 0), 33, 20),
+    ((1, 4, 64, 64), (8, 4, 3, 3), (4, 4), (1, 1), 64, 32),
+    ((1, 5, 8, 8), (16, 5, 3, 3), (1, 1), (1, 1), 48, 48),
 ])
 def test_conv_attention_shapes(lc, oracle, xs, ws, stride, pad, seq, hd):
     x, w = synth.normal(xs, stream=40), synth.normal(ws, std=0.3, stream=41)
