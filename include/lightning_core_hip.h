@@ -435,9 +435,32 @@ lcError_t lcHipTimerDestroy(lcHipTimer* t);
 lcError_t lcHipTimerStart(lcHipTimer* t);
 lcError_t lcHipTimerStop(lcHipTimer* t, float* elapsed_ms);
 
-/* Saves / loads the gfx950 tune cache (#lc_tune_cache,matmul,2 CSV). */
+/* The gfx950 matmul tune cache: the reference's file convention
+ * (src/ops/matmul_metal.mm:133-139, :416-517) with rows re-keyed for gfx950
+ * (m,k,n,dtype,arch,kernel variant).  It is also loaded implicitly on the
+ * first matmul (CJ_MATMUL_TUNE_CACHE_FILE, else
+ * .lightning_core_matmul_tune_cache.csv in the working directory) and
+ * rewritten when a new shape is tuned; versions 1 and 2 are read, 2 written.
+ * Load makes `path` the cache file; a header of another kind or version
+ * clears the table and returns LC_INVALID_VALUE. */
 lcError_t lcHipTuneCacheSave(const char* path);
 lcError_t lcHipTuneCacheLoad(const char* path);
+size_t lcHipTuneCacheSize(void);
+
+/* The attention tune cache (src/attention_metal.mm:184-336, same layout:
+ * F,seq,dim,causal,resident_hint,sync_hint,mode and T rows with compute_loss);
+ * the mode is the gfx950 fp32 kernel's split count (1, 2, 4, 8).  Implicit
+ * file: CJ_ATTN_TUNE_CACHE_FILE, else .lightning_core_attn_tune_cache.csv. */
+lcError_t lcHipAttentionTuneCacheSave(const char* path);
+lcError_t lcHipAttentionTuneCacheLoad(const char* path);
+lcError_t lcHipAttentionResetTuning(void);
+size_t lcHipAttentionTuneCacheSize(void);
+
+/* runtime::preloadRuntimeProfileEnv (core/runtime.hpp:193,
+ * src/runtime.cpp:101-168, :421-423): imports CJ_* variables from the runtime
+ * profile file once per process (CJ_RUNTIME_PROFILE_ENV_FILE or the
+ * reference's cwd-relative candidates; CJ_RUNTIME_PROFILE_AUTOLOAD=0 skips). */
+void lcPreloadRuntimeProfileEnv(void);
 
 #ifdef __cplusplus
 }

@@ -10,11 +10,14 @@
 // The reference's CPU paths (device cpu, the one-shot CPU crossover and the
 // kNotSupported -> CPU fallback) belong to the reference's own dispatcher; in
 // this library a request that the HIP kernels cannot serve returns an error.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <memory>
+#include <vector>
 
 #include "ops_internal.hpp"
+#include "tune.hpp"
 
 namespace lchip {
 
@@ -75,6 +78,155 @@ bool postIsIdentity(const lcAttentionIoPolicy& p) {
   return p.output_scale == 1.0f && p.output_bias == 0.0f && !p.output_relu;
 }
 
+// Median time of each candidate launch, timed round-robin (one warm-up
+// round, then 3 rounds; HIP events on the context stream) so that clock
+// drift spreads over all candidates.  The reference's forward autotune takes
+// a 3-sample median per mode (src/attention_metal.mm:1517-1574).
+template <typename Launch>
+Status timeCandidates(HipContext* ctx, const std::vector<int>& cands, Launch launch, std::vector<float>* ms) {
+  constexpr int kRounds = 3;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  LC_HIP_TRY(hipEventCreate(&e0));
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return failHip(hipErrorOutOfMemory, "attention autotune events");
+  }
+  std::vector<std::vector<float>> samples(cands.size());
+  hipError_t e = hipSuccess;
+  for (int round = -1; round < kRounds && e == hipSuccess; ++round) {
+    for (std::size_t c = 0; c < cands.size() && e == hipSuccess; ++c) {
+      e = hipEventRecord(e0, ctx->stream);
+      if (e == hipSuccess) e = launch(cands[c]);
+      if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+      if (e == hipSuccess) e = hipEventSynchronize(e1);
+      float t = 0.0f;
+      if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+      if (round >= 0) {
+        samples[c].push_back(t);
+      }
+    }
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (e != hipSuccess) {
+    return failHip(e, "attention autotune");
+  }
+  ms->clear();
+  for (auto& v : samples) {
+    std::sort(v.begin(), v.end());
+    ms->push_back(v[v.size() / 2]);
+  }
+  return Status::kSuccess;
+}
+
+// The heuristic's split count stays unless another is faster by 3%.
+int pickSplits(const std::vector<int>& cands, const std::vector<float>& ms, int heuristic) {
+  float ref = 0.0f;
+  for (std::size_t c = 0; c < cands.size(); ++c) {
+    if (cands[c] == heuristic) {
+      ref = ms[c];
+    }
+  }
+  int best = heuristic;
+  float best_ms = ref > 0.0f ? ref * 0.97f : 0.0f;
+  for (std::size_t c = 0; c < cands.size(); ++c) {
+    if (best_ms <= 0.0f || ms[c] < best_ms) {
+      best_ms = ms[c];
+      best = cands[c];
+    }
+  }
+  return best;
+}
+
+// Split counts worth timing for one head: the valid ones (LDS limits) up to
+// the number of 32-key tiles.
+std::vector<int> splitCandidates(int S, int D) {
+  const int tiles = (S + 31) / 32;
+  std::vector<int> c;
+  for (int ks = 1; ks <= 8; ks *= 2) {
+    if (kern::attentionF32Splits(1, S, D, ks) == ks && (ks == 1 || ks <= tiles)) {
+      c.push_back(ks);
+    }
+  }
+  return c;
+}
+
+// The fp32 single-head forward's split count for this key: the tune cache,
+// else the fastest candidate (CJ_ATTN_AUTOTUNE not off), else the heuristic
+// (src/attention_metal.mm:1483-1583 is the reference's forward autotune).
+Status forwardSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, const lcAttentionIoPolicy& policy,
+                     int* splits) {
+  AttnTuneKey key;
+  key.kind = 'F';
+  key.seq = sh.seq_len;
+  key.dim = sh.head_dim;
+  key.causal = sh.causal ? 1 : 0;
+  key.resident_hint = (!policy.upload_q && !policy.upload_k && !policy.upload_v && !policy.download_out) ? 1 : 0;
+  key.sync_hint = policy.synchronize ? 1 : 0;
+  if (attnTuneLookup(key, splits)) {
+    return Status::kSuccess;
+  }
+  const int S = static_cast<int>(sh.seq_len);
+  const int D = static_cast<int>(sh.head_dim);
+  int best = kern::attentionF32Splits(1, S, D, 0);
+  const std::vector<int> cands = splitCandidates(S, D);
+  if (cands.size() > 1 && autotuneEnabled("CJ_ATTN_AUTOTUNE")) {
+    std::vector<float> ms;
+    LC_TRY(timeCandidates(
+        ctx, cands,
+        [&](int ks) {
+          return kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(), 1,
+                                    S, D, sh.causal, policy.output_scale, policy.output_bias, policy.output_relu,
+                                    nullptr, ctx->stream, ks);
+        },
+        &ms));
+    best = pickSplits(cands, ms, best);
+  }
+  attnTuneRecord(key, best);
+  *splits = best;
+  return Status::kSuccess;
+}
+
+// The train step's dV split count (T rows; src/attention_metal.mm:1700-1830
+// tunes the reference's train modes).  Candidates run on a copy of V: the
+// kernel updates V in place.
+Status trainSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, const lcAttentionIoPolicy& policy,
+                   bool compute_loss, float lr, int* splits) {
+  AttnTuneKey key;
+  key.kind = 'T';
+  key.seq = sh.seq_len;
+  key.dim = sh.head_dim;
+  key.causal = sh.causal ? 1 : 0;
+  key.resident_hint = (!policy.upload_q && !policy.upload_k && !policy.upload_v && !policy.download_v) ? 1 : 0;
+  key.sync_hint = policy.synchronize ? 1 : 0;
+  key.compute_loss = compute_loss ? 1 : 0;
+  if (attnTuneLookup(key, splits)) {
+    return Status::kSuccess;
+  }
+  const int S = static_cast<int>(sh.seq_len);
+  const int D = static_cast<int>(sh.head_dim);
+  int best = kern::attentionF32Splits(1, S, D, 0);
+  const std::vector<int> cands = splitCandidates(S, D);
+  if (cands.size() > 1 && autotuneEnabled("CJ_ATTN_AUTOTUNE")) {
+    const std::size_t bytes = sh.elems() * sizeof(float);
+    LC_TRY(res.v_scratch.ensure(bytes));
+    LC_HIP_TRY(hipMemcpyAsync(res.v_scratch.get(), res.v.get(), bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    std::vector<float> ms;
+    LC_TRY(timeCandidates(
+        ctx, cands,
+        [&](int ks) {
+          return kern::attentionDvUpdateF32(res.q.as<float>(), res.k.as<float>(), res.v_scratch.as<float>(),
+                                            res.out.as<float>(), res.target.as<float>(), res.stats.as<float>(), 1, S,
+                                            D, sh.causal, lr, ctx->stream, ks);
+        },
+        &ms));
+    best = pickSplits(cands, ms, best);
+  }
+  attnTuneRecord(key, best);
+  *splits = best;
+  return Status::kSuccess;
+}
+
 }  // namespace
 
 Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnShape& sh, const float* q,
@@ -124,13 +276,17 @@ Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnSh
   const int D = static_cast<int>(sh.head_dim);
   const int bh = static_cast<int>(sh.bh());
   const std::size_t hint = sh.seq_len * sh.seq_len * sh.head_dim;
+  int splits = 0;  // batched fp32 heads keep the heuristic (the cache keys one head)
+  if (!half && bh == 1 && repeat > 0) {
+    LC_TRY(forwardSplits(ctx, res, sh, policy, &splits));
+  }
   for (std::size_t r = 0; r < repeat; ++r) {
     traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, hint);
     hipError_t e;
     if (!half) {
       e = kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(), bh, S, D,
                              sh.causal, policy.output_scale, policy.output_bias, policy.output_relu, nullptr,
-                             ctx->stream);
+                             ctx->stream, splits);
     } else {
       e = kern::attentionHalf(res.q.as<uint16_t>(), res.k.as<uint16_t>(), res.v.as<uint16_t>(), res.out.as<float>(),
                               nullptr, static_cast<int>(sh.heads), bh, S, static_cast<int>(sh.sPad()), D, sh.causal,
@@ -212,11 +368,14 @@ Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShap
     e = kern::mseLossF32(res.out.as<float>(), res.target.as<float>(), n,
                          1.0f / static_cast<float>(sh.seq_len * sh.head_dim), res.loss.as<float>(), ctx->stream);
   }
-  if (e == hipSuccess) {
-    e = kern::attentionDvUpdateF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(),
-                                   res.target.as<float>(), res.stats.as<float>(), 1, S, D, sh.causal, learning_rate,
-                                   ctx->stream);
+  if (e != hipSuccess) {
+    return failHip(e, "attention train step launch");
   }
+  int splits = 0;
+  LC_TRY(trainSplits(ctx, res, sh, policy, loss_out != nullptr, learning_rate, &splits));
+  e = kern::attentionDvUpdateF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(),
+                                 res.target.as<float>(), res.stats.as<float>(), 1, S, D, sh.causal, learning_rate,
+                                 ctx->stream, splits);
   if (e != hipSuccess) {
     return failHip(e, "attention train step launch");
   }

@@ -171,7 +171,7 @@ Status vitForwardDevice(HipContext* ctx, lcVitBlockSession* s) {
   }
   traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, s->M * c.embed * c.embed);
   e = kern::gemmHalfTN(s->attn16.as<uint16_t>(), s->wo_t16.as<uint16_t>(), s->out.as<float>(), M, E, E, E, E, E, ht,
-                       ctx->stream);
+                       kern::GemmHalfVariant::kAuto, ctx->stream);
   return e == hipSuccess ? Status::kSuccess : failHip(e, "vit out-projection launch");
 }
 

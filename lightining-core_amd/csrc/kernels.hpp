@@ -31,8 +31,13 @@ hipError_t gemmF32(const float* A, const float* B, float* C, int M, int N, int K
 // over at most max_groups workgroups: `part` holds max_groups * 4096 floats
 // of partial tiles and `flags` max_groups ints, zero before the first call
 // (each call leaves them zero).  Calls that share part/flags must not overlap.
+// Variants: whole 64x64 tiles per workgroup (BK 64 or 32), or stream-K
+// (BK 64); kAuto takes CJ_HIP_GEMM_F32=dp|sk|bk32, else the heuristic of
+// gemmF32Choose.
+enum class GemmF32Variant { kAuto = 0, kDataParallel = 1, kStreamK = 2, kDataParallelBK32 = 3 };
+GemmF32Variant gemmF32Choose(int M, int N, int max_groups);
 hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
-                         float* part, int* flags, int max_groups, hipStream_t stream);
+                         float* part, int* flags, int max_groups, GemmF32Variant variant, hipStream_t stream);
 // dst[r][c] = src[r][c] (row stride ld_src) for r < rows, c < cols; 0 up to
 // rows_pad x cols_pad (dst row stride cols_pad).
 hipError_t padCopyF32(const float* src, float* dst, int rows, int cols, size_t ld_src, int rows_pad, int cols_pad,
@@ -59,7 +64,11 @@ hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu,
 // log2 domain (p = exp2((q.k)*scale*log2(e) - m) / l).
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D,
                         bool causal, float post_scale, float post_bias, int post_relu, float* stats,
-                        hipStream_t stream);
+                        hipStream_t stream, int splits = 0);
+// Key splits (waves per 32 queries) attentionF32 / attentionDvUpdateF32 use:
+// `requested` (1, 2, 4 or 8) limited to what the head dim allows, or the
+// heuristic when requested is 0.
+int attentionF32Splits(int bh, int S, int D, int requested);
 // The reference's conv -> attention chain in one launch: conv2d NCHW (+bias,
 // ReLU) of x [batch, cin, h, wd] with w [cout, cin, kh, kw], Q/K/V = the
 // consecutive S*D slices of its flat output repeated to 3*S*D values, then
@@ -76,7 +85,7 @@ bool convAttentionStagesInputs(int batch, int cin, int h, int wd, int cout, int 
 // P recomputed from q, k and the forward's stats.
 hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const float* out, const float* target,
                                 const float* stats, int bh, int S, int D, bool causal, float lr,
-                                hipStream_t stream);
+                                hipStream_t stream, int splits = 0);
 // *loss = norm * sum_i (out_i - target_i)^2 (one workgroup, fixed order).
 hipError_t mseLossF32(const float* out, const float* target, size_t n, float norm, float* loss, hipStream_t stream);
 
@@ -94,9 +103,14 @@ hipError_t convertTransposePad(const float* src, uint16_t* dst, int batch, int r
 
 // C[M,N] (fp32, ldc) = A[M,K] . Bt[N,K]^T with A, Bt 16-bit row-major (lda,
 // ldb), K a multiple of kHalfGemmBK, A readable up to roundup(M, 256) rows and
-// Bt up to roundup(N, 256) rows.
+// Bt up to roundup(N, 256) rows.  Variants (block tile, waves): kLds 256x256
+// with direct global->LDS loads, kBig8 / kBig4 256x256 with 8 / 4 waves, kMid
+// 128x128, kSmall 64x64, kSkinny for M <= 16; kAuto follows gemmHalfChoose
+// (CJ_HIP_GEMM_TILE=lds|big8|big4|mid|small overrides it).
+enum class GemmHalfVariant { kAuto = 0, kLds = 1, kBig8 = 2, kBig4 = 3, kMid = 4, kSmall = 5, kSkinny = 6 };
+GemmHalfVariant gemmHalfChoose(int M, int N);
 hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda, int ldb,
-                      int ldc, Half t, hipStream_t stream);
+                      int ldc, Half t, GemmHalfVariant variant, hipStream_t stream);
 // Same GEMM with a 16-bit output (optionally ReLU).
 hipError_t gemmHalfTNHalfOut(const uint16_t* A, const uint16_t* Bt, uint16_t* C, int M, int N, int K, int lda,
                              int ldb, int ldc, int relu, Half t, hipStream_t stream);

@@ -981,8 +981,31 @@ namespace lchip::kern {
 
 using namespace lchip::k;
 
+int attentionF32Splits(int bh, int S, int D, int requested) {
+  const int nqb = (S + 31) / 32;
+  const int dt = (D + 31) / 32;
+  // Per-wave K + V tiles must fit the 160 KB of LDS: up to 8 splits at
+  // DT <= 2 (140 KB), 2 at DT <= 4, 1 beyond (the launch switches below).
+  const int cap = dt <= 2 ? 8 : (dt <= 4 ? 2 : 1);
+  if (requested > 0) {
+    int ks = 1;
+    while (ks * 2 <= requested && ks * 2 <= cap) {
+      ks *= 2;
+    }
+    return ks;
+  }
+  // Heuristic: enough waves for about two per CU, at most one split per
+  // 32-key tile.
+  int ks = 1;
+  while (ks < cap && static_cast<long long>(nqb) * bh * ks * 2 <= 512 && ks * 2 <= nqb) {
+    ks *= 2;
+  }
+  return ks;
+}
+
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D, bool causal,
-                        float post_scale, float post_bias, int post_relu, float* stats, hipStream_t stream) {
+                        float post_scale, float post_bias, int post_relu, float* stats, hipStream_t stream,
+                        int splits) {
   if (D <= 0 || D > 256 || S <= 0 || bh <= 0) {
     return hipErrorInvalidValue;
   }
@@ -991,15 +1014,7 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
   const dim3 grid(nqb, bh);
   const int dt = (D + 31) / 32;
   const int cz = causal ? 1 : 0;
-  // Key splits: enough waves for about two per CU, at most one split per
-  // 32-key tile, and K + V tiles of every wave within the 160 KB of LDS
-  // (8 splits at DT = 2: 140 KB).
-  const int tiles = nqb;
-  int ks = 1;
-  while (ks < 8 && static_cast<long long>(nqb) * bh * ks * 2 <= 512 && ks * 2 <= tiles &&
-         (ks * 2) * dt <= (dt <= 2 ? 16 : 8)) {
-    ks *= 2;
-  }
+  const int ks = attentionF32Splits(bh, S, D, splits);
   const bool vec = dt <= 2 && D % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(v) % 16 == 0;
   const AttnSrcGlobal src{q, k, v};
@@ -1094,7 +1109,7 @@ hipError_t convAttentionF32(const float* x, const float* w, const float* bias, i
 
 hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const float* out, const float* target,
                                 const float* stats, int bh, int S, int D, bool causal, float lr,
-                                hipStream_t stream) {
+                                hipStream_t stream, int splits) {
   if (D <= 0 || D > 256 || S <= 0 || bh <= 0) {
     return hipErrorInvalidValue;
   }
@@ -1103,13 +1118,9 @@ hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const 
   const dim3 grid(nkb, bh);
   const int dt = (D + 31) / 32;
   const int cz = causal ? 1 : 0;
-  // Query-tile splits: as many as fit (LDS: K tile + per-wave Q / dO tiles)
-  // while the grid stays below about two waves per CU.
-  int ks = 1;
-  while (ks < 8 && static_cast<long long>(nkb) * bh * ks * 2 <= 512 && ks * 2 <= nkb &&
-         (ks * 2) * dt <= (dt <= 2 ? 16 : 8)) {
-    ks *= 2;
-  }
+  // Query-tile splits: the same rule and LDS limits as the forward's key
+  // splits (K tile + per-wave Q / dO tiles).
+  const int ks = attentionF32Splits(bh, S, D, splits);
 #define LC_DV_F32(DT_, KS_)                                                                                         \
   hipLaunchKernelGGL((attn_dv_f32_kernel<DT_, KS_>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out, target, stats, \
                      S, D, cz, scale, lr)

@@ -1042,9 +1042,9 @@ static hipError_t launch_gemm_half_cfg(LoadA load_a, const uint16_t* Bt, int M, 
 }
 
 template <typename T, typename LoadA, typename Epi>
-static hipError_t launch_gemm_half(LoadA load_a, const uint16_t* Bt, int M, int N, int K, int ldb, Epi epi,
-                                   hipStream_t stream) {
-  switch (pick_half_tile(M, N, false)) {
+static hipError_t launch_gemm_half_tile(HalfTile tile, LoadA load_a, const uint16_t* Bt, int M, int N, int K,
+                                        int ldb, Epi epi, hipStream_t stream) {
+  switch (tile) {
     case HalfTile::kLds:
     case HalfTile::kBig8:
       return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
@@ -1056,6 +1056,12 @@ static hipError_t launch_gemm_half(LoadA load_a, const uint16_t* Bt, int M, int 
     default:
       return launch_gemm_half_cfg<T, 64, 64, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
   }
+}
+
+template <typename T, typename LoadA, typename Epi>
+static hipError_t launch_gemm_half(LoadA load_a, const uint16_t* Bt, int M, int N, int K, int ldb, Epi epi,
+                                   hipStream_t stream) {
+  return launch_gemm_half_tile<T>(pick_half_tile(M, N, false), load_a, Bt, M, N, K, ldb, epi, stream);
 }
 
 template <typename T, int WM, int WN>
@@ -1079,32 +1085,40 @@ hipError_t gemmF32(const float* A, const float* B, float* C, int M, int N, int K
   return launch_gemm_f32<false>(A, B, M, N, K, lda, ldb, EpiStoreF32{C, ldc}, stream);
 }
 
+GemmF32Variant gemmF32Choose(int M, int N, int max_groups) {
+  const char* env = getenv("CJ_HIP_GEMM_F32");
+  const std::string v = env != nullptr ? env : "";
+  if (v == "dp") return GemmF32Variant::kDataParallel;
+  if (v == "sk") return GemmF32Variant::kStreamK;
+  if (v == "bk32") return GemmF32Variant::kDataParallelBK32;
+  // Whole tiles per workgroup when they fill the CUs evenly (or there are
+  // many of them); stream-K otherwise.
+  const int tiles = ((M + 63) / 64) * ((N + 63) / 64);
+  return (tiles % max_groups != 0 && tiles < 8 * max_groups) ? GemmF32Variant::kStreamK
+                                                              : GemmF32Variant::kDataParallel;
+}
+
 hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
-                         float* part, int* flags, int max_groups, hipStream_t stream) {
+                         float* part, int* flags, int max_groups, GemmF32Variant variant, hipStream_t stream) {
   if (K <= 0 || K % kF32GemmBK != 0 || lda % 4 != 0 || ldb % 4 != 0 || M <= 0 || N <= 0 || max_groups <= 0) {
     return hipErrorInvalidValue;
   }
   const int tiles_m = (M + 63) / 64;
   const int tiles_n = (N + 63) / 64;
-  const char* env = getenv("CJ_HIP_GEMM_F32");
-  const std::string v = env != nullptr ? env : "";
-  const int bk = v == "bk32" ? 32 : 64;
+  if (variant == GemmF32Variant::kAuto) {
+    variant = gemmF32Choose(M, N, max_groups);
+  }
+  const bool bk32 = variant == GemmF32Variant::kDataParallelBK32;
+  const int bk = bk32 ? 32 : 64;
   const int nk = K / bk;
   const int tiles = tiles_m * tiles_n;
-  // Whole tiles per workgroup when they fill the CUs evenly (or there are
-  // many of them); stream-K otherwise.
-  const bool sk = v == "sk" || (v != "dp" && tiles % max_groups != 0 && tiles < 8 * max_groups);
+  const bool sk = variant == GemmF32Variant::kStreamK;
   const long long iters = static_cast<long long>(tiles) * nk;
   const int groups = sk ? static_cast<int>(iters < max_groups ? iters : max_groups) : tiles;
   const EpiStoreF32 epi{C, ldc};
-  if (v == "bk32") {
-    if (sk) {
-      hipLaunchKernelGGL((gemm_f32_lds_kernel<32, 4, 2, true, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A,
-                         B, M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
-    } else {
-      hipLaunchKernelGGL((gemm_f32_lds_kernel<32, 4, 2, false, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A,
-                         B, M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
-    }
+  if (bk32) {
+    hipLaunchKernelGGL((gemm_f32_lds_kernel<32, 4, 2, false, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A,
+                       B, M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
   } else if (sk) {
     hipLaunchKernelGGL((gemm_f32_lds_kernel<64, 4, 2, true, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A, B,
                        M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
@@ -1120,17 +1134,36 @@ hipError_t gemmF32ConvNchw(const float* cols, const float* Wt, float* out, int M
   return launch_gemm_f32<true>(cols, Wt, M, N, K, K, K, EpiConvNchwF32{out, bias, relu, N, ohw}, stream);
 }
 
+GemmHalfVariant gemmHalfChoose(int M, int N) {
+  if (M <= 16) {
+    return GemmHalfVariant::kSkinny;
+  }
+  switch (pick_half_tile(M, N, true)) {
+    case HalfTile::kLds: return GemmHalfVariant::kLds;
+    case HalfTile::kBig8: return GemmHalfVariant::kBig8;
+    case HalfTile::kBig4: return GemmHalfVariant::kBig4;
+    case HalfTile::kMid: return GemmHalfVariant::kMid;
+    default: return GemmHalfVariant::kSmall;
+  }
+}
+
 hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda, int ldb, int ldc,
-                      Half t, hipStream_t stream) {
+                      Half t, GemmHalfVariant variant, hipStream_t stream) {
   if (K % kHBK != 0) {
     return hipErrorInvalidValue;
   }
+  if (variant == GemmHalfVariant::kAuto) {
+    variant = gemmHalfChoose(M, N);
+  }
+  if (variant == GemmHalfVariant::kSkinny && M > 16) {
+    return hipErrorInvalidValue;  // the skinny kernel holds at most 16 rows of A
+  }
   // A and Bt come from the resident upload, padded to 256 rows.
-  if (M > 16 && K > 0 && pick_half_tile(M, N, true) == HalfTile::kLds) {
+  if (variant == GemmHalfVariant::kLds && K > 0) {
     return t == Half::kBF16 ? launch_gemm_lds<BF16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
                             : launch_gemm_lds<F16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
   }
-  if (M <= 16) {
+  if (variant == GemmHalfVariant::kSkinny) {
     // Bt must be readable up to roundup(N, 32) rows (callers pad to 256).
     constexpr int NT = 2;
     constexpr int WAVES = 4;
@@ -1145,10 +1178,14 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
     return hipGetLastError();
   }
   const LoadRowMajor la{A, lda};
+  const HalfTile tile = variant == GemmHalfVariant::kBig4  ? HalfTile::kBig4
+                        : variant == GemmHalfVariant::kMid ? HalfTile::kMid
+                        : variant == GemmHalfVariant::kSmall ? HalfTile::kSmall
+                                                             : HalfTile::kBig8;
   if (t == Half::kBF16) {
-    return launch_gemm_half<BF16>(la, Bt, M, N, K, ldb, EpiF32{C, ldc}, stream);
+    return launch_gemm_half_tile<BF16>(tile, la, Bt, M, N, K, ldb, EpiF32{C, ldc}, stream);
   }
-  return launch_gemm_half<F16>(la, Bt, M, N, K, ldb, EpiF32{C, ldc}, stream);
+  return launch_gemm_half_tile<F16>(tile, la, Bt, M, N, K, ldb, EpiF32{C, ldc}, stream);
 }
 
 hipError_t gemmHalfTNHalfOut(const uint16_t* A, const uint16_t* Bt, uint16_t* C, int M, int N, int K, int lda,

@@ -13,7 +13,12 @@
 //     their own buffers instead.
 // 16-bit compute rounds the fp32 host data once at upload (RNE) and lays B out
 // K-contiguous (transposed), the layout the MFMA GEMM reads.
+#include <algorithm>
+#include <cstdlib>
 #include <cstring>
+#include <iterator>
+#include <string>
+#include <vector>
 
 #include "ops_internal.hpp"
 #include "tune.hpp"
@@ -71,46 +76,72 @@ Status uploadB(HipContext* ctx, MatMulResident& r, const float* b) {
   return e == hipSuccess ? Status::kSuccess : failHip(e, "matmul upload conversion (B)");
 }
 
-// The kernel configuration the dispatch below selects for a shape (recorded
-// in the tune cache so it can be saved, inspected and reset).
-TuneEntry gemmConfig(const MatMulResident& r) {
+// Tune-cache names of the GEMM variants and the configuration each stands
+// for (block tile M x N x K, waves, K-split of a stage between wave groups).
+struct VariantInfo {
+  int variant;
+  const char* name;
+  int tile_m, tile_n, tile_k, waves, split_k;
+};
+
+constexpr VariantInfo kF32Variants[] = {
+    {static_cast<int>(kern::GemmF32Variant::kDataParallel), "f32_dp_64x64x64", 64, 64, 64, 8, 2},
+    {static_cast<int>(kern::GemmF32Variant::kStreamK), "f32_streamk_64x64x64", 64, 64, 64, 8, 2},
+    {static_cast<int>(kern::GemmF32Variant::kDataParallelBK32), "f32_dp_64x64x32", 64, 64, 32, 8, 2},
+};
+
+constexpr VariantInfo kHalfVariants[] = {
+    {static_cast<int>(kern::GemmHalfVariant::kLds), "half_lds_256x256", 256, 256, 64, 8, 1},
+    {static_cast<int>(kern::GemmHalfVariant::kBig8), "half_big8_256x256", 256, 256, 64, 8, 1},
+    {static_cast<int>(kern::GemmHalfVariant::kBig4), "half_big4_256x256", 256, 256, 64, 4, 1},
+    {static_cast<int>(kern::GemmHalfVariant::kMid), "half_mid_128x128", 128, 128, 64, 4, 1},
+    {static_cast<int>(kern::GemmHalfVariant::kSmall), "half_small_64x64", 64, 64, 64, 4, 1},
+    {static_cast<int>(kern::GemmHalfVariant::kSkinny), "half_skinny_16x32", 16, 32, 32, 4, 4},
+};
+
+struct VariantTable {
+  const VariantInfo* first;
+  const VariantInfo* last;
+  const VariantInfo* begin() const { return first; }
+  const VariantInfo* end() const { return last; }
+};
+
+VariantTable variants(bool half) {
+  return half ? VariantTable{std::begin(kHalfVariants), std::end(kHalfVariants)}
+              : VariantTable{std::begin(kF32Variants), std::end(kF32Variants)};
+}
+
+TuneEntry entryFor(bool half, int variant) {
   TuneEntry e;
-  if (!isHalf(r.dtype)) {
-    e.kernel = "f32_lds_32x32x2";
-    e.tile_m = kern::kF32GemmBM;
-    e.tile_n = kern::kF32GemmBN;
-    e.tile_k = kern::kF32GemmBK;
-    e.waves = 8;
-    e.split_k = 2;  // two wave groups per block, one per K half of each stage
-  } else if (r.m <= 16) {
-    e.kernel = "half_skinny_16x16x32";
-    e.tile_m = 16;
-    e.tile_n = 32;
-    e.tile_k = 32;
-    e.waves = 4;
-    e.split_k = 4;
-  } else {
-    // mirrors pick_half_tile() in kernels/gemm.hip
-    const auto tiles = [&](std::size_t b) { return ((r.m + b - 1) / b) * ((r.n + b - 1) / b); };
-    e.kernel = "half_tn_32x32x16";
-    if (tiles(256) >= 256) {
-      e.tile_m = e.tile_n = 256;
-      e.tile_k = 64;
-      e.waves = 8;
-    } else if (tiles(128) >= 256) {
-      e.tile_m = e.tile_n = 128;
-      e.tile_k = 64;
-      e.waves = 4;
-    } else {
-      e.tile_m = e.tile_n = 64;
-      e.tile_k = 64;
-      e.waves = 4;
+  for (const VariantInfo& v : variants(half)) {
+    if (v.variant == variant) {
+      e.kernel = v.name;
+      e.tile_m = v.tile_m;
+      e.tile_n = v.tile_n;
+      e.tile_k = v.tile_k;
+      e.waves = v.waves;
+      e.split_k = v.split_k;
     }
   }
   return e;
 }
 
-hipError_t launchGemm(HipContext* ctx, MatMulResident& r) {
+// A cached entry names a variant this shape can run (else it is ignored).
+bool variantFromEntry(const TuneEntry& e, bool half, std::size_t m, int* variant) {
+  for (const VariantInfo& v : variants(half)) {
+    if (e.kernel == v.name) {
+      const bool skinny = v.variant == static_cast<int>(kern::GemmHalfVariant::kSkinny);
+      if (half && skinny != (m <= 16)) {
+        return false;
+      }
+      *variant = v.variant;
+      return true;
+    }
+  }
+  return false;
+}
+
+hipError_t launchGemm(HipContext* ctx, MatMulResident& r, int variant) {
   const int M = static_cast<int>(r.m);
   const int K = static_cast<int>(r.k);
   const int N = static_cast<int>(r.n);
@@ -124,11 +155,111 @@ hipError_t launchGemm(HipContext* ctx, MatMulResident& r) {
       return hipErrorOutOfMemory;
     }
     return kern::gemmF32Padded(r.a.as<float>(), r.b.as<float>(), r.c.as<float>(), M, N, kp, kp, np, N,
-                               ctx->gemm_part.as<float>(), ctx->gemm_flags.as<int>(), groups, ctx->stream);
+                               ctx->gemm_part.as<float>(), ctx->gemm_flags.as<int>(), groups,
+                               static_cast<kern::GemmF32Variant>(variant), ctx->stream);
   }
   const int kp = static_cast<int>(roundUp(r.k, kern::kHalfGemmBK));
   return kern::gemmHalfTN(r.a.as<uint16_t>(), r.b.as<uint16_t>(), r.c.as<float>(), M, N, kp, kp, kp, N,
-                          halfOf(r.dtype), ctx->stream);
+                          halfOf(r.dtype), static_cast<kern::GemmHalfVariant>(variant), ctx->stream);
+}
+
+// Times the candidates round-robin (so clock and thermal drift spread over
+// all of them): one warm-up round, then 5 rounds of 2 back-to-back launches
+// per candidate timed with HIP events on the context stream; the median per
+// candidate counts (the reference's autoTuneTile takes a 5-sample median,
+// src/ops/matmul_metal.mm:1687-1710).
+Status timeVariants(HipContext* ctx, MatMulResident& r, const std::vector<int>& cands, std::vector<float>* ms) {
+  constexpr int kRounds = 5;
+  constexpr int kLaunches = 2;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  LC_HIP_TRY(hipEventCreate(&e0));
+  if (hipEventCreate(&e1) != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return failHip(hipErrorOutOfMemory, "matmul autotune events");
+  }
+  std::vector<std::vector<float>> samples(cands.size());
+  hipError_t e = hipSuccess;
+  for (int round = -1; round < kRounds && e == hipSuccess; ++round) {
+    for (std::size_t c = 0; c < cands.size() && e == hipSuccess; ++c) {
+      e = hipEventRecord(e0, ctx->stream);
+      for (int l = 0; l < kLaunches && e == hipSuccess; ++l) {
+        e = launchGemm(ctx, r, cands[c]);
+      }
+      if (e == hipSuccess) e = hipEventRecord(e1, ctx->stream);
+      if (e == hipSuccess) e = hipEventSynchronize(e1);
+      float t = 0.0f;
+      if (e == hipSuccess) e = hipEventElapsedTime(&t, e0, e1);
+      if (round >= 0) {
+        samples[c].push_back(t);
+      }
+    }
+  }
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (e != hipSuccess) {
+    return failHip(e, "matmul autotune");
+  }
+  ms->clear();
+  for (auto& v : samples) {
+    std::sort(v.begin(), v.end());
+    ms->push_back(v[v.size() / 2]);
+  }
+  return Status::kSuccess;
+}
+
+// Settles r.variant for the shape: a tune-cache entry, else (CJ_MATMUL_AUTOTUNE
+// not off) the fastest candidate, else the heuristic; the choice is recorded.
+// CJ_HIP_GEMM_F32 / CJ_HIP_GEMM_TILE (sweep overrides) bypass all of it.
+Status settleVariant(HipContext* ctx, MatMulResident& r) {
+  const bool half = isHalf(r.dtype);
+  r.variant = 0;
+  if (std::getenv(half ? "CJ_HIP_GEMM_TILE" : "CJ_HIP_GEMM_F32") != nullptr) {
+    return Status::kSuccess;
+  }
+  // base architecture ("gfx950"), without the target features after ':'
+  std::string arch = ctx->props.gcnArchName;
+  arch = arch.substr(0, arch.find(':'));
+  const int dtype = static_cast<int>(r.dtype);
+  TuneEntry known;
+  if (tuneLookup(r.m, r.k, r.n, dtype, arch, &known) && variantFromEntry(known, half, r.m, &r.variant)) {
+    return Status::kSuccess;
+  }
+  const int M = static_cast<int>(r.m);
+  const int N = static_cast<int>(r.n);
+  const int groups = ctx->props.multiProcessorCount > 0 ? ctx->props.multiProcessorCount : 256;
+  int best = half ? static_cast<int>(kern::gemmHalfChoose(M, N)) : static_cast<int>(kern::gemmF32Choose(M, N, groups));
+  std::vector<int> cands;
+  if (!half) {
+    cands = {static_cast<int>(kern::GemmF32Variant::kDataParallel), static_cast<int>(kern::GemmF32Variant::kStreamK)};
+  } else if (r.m > 16) {
+    for (const VariantInfo& v : kHalfVariants) {
+      if (v.variant != static_cast<int>(kern::GemmHalfVariant::kSkinny)) {
+        cands.push_back(v.variant);
+      }
+    }
+  }
+  if (cands.size() > 1 && autotuneEnabled("CJ_MATMUL_AUTOTUNE")) {
+    std::vector<float> ms;
+    LC_TRY(timeVariants(ctx, r, cands, &ms));
+    // The heuristic's choice stays unless another variant is clearly faster
+    // (3%: below that the measurement cannot tell them apart).
+    float ref_ms = 0.0f;
+    for (std::size_t c = 0; c < cands.size(); ++c) {
+      if (cands[c] == best) {
+        ref_ms = ms[c];
+      }
+    }
+    float best_ms = ref_ms > 0.0f ? ref_ms * 0.97f : 0.0f;
+    for (std::size_t c = 0; c < cands.size(); ++c) {
+      if (best_ms <= 0.0f || ms[c] < best_ms) {
+        best_ms = ms[c];
+        best = cands[c];
+      }
+    }
+  }
+  r.variant = best;
+  tuneRecord(r.m, r.k, r.n, dtype, arch, entryFor(half, best));
+  return Status::kSuccess;
 }
 
 }  // namespace
@@ -149,6 +280,7 @@ Status matmulResident(HipContext* ctx, MatMulResident& r, std::size_t m, std::si
   }
   if (r.m != m || r.k != k || r.n != n || r.dtype != dtype) {
     r.has_a = r.has_b = r.has_c = false;
+    r.tuned = false;
     r.m = m;
     r.k = k;
     r.n = n;
@@ -167,13 +299,13 @@ Status matmulResident(HipContext* ctx, MatMulResident& r, std::size_t m, std::si
   }
   LC_TRY(r.c.ensure(m * n * sizeof(float)));
   const std::size_t hint = m * k * n;
-  TuneEntry known;
-  if (!tuneLookup(m, k, n, static_cast<int>(dtype), ctx->props.gcnArchName, &known)) {
-    tuneRecord(m, k, n, static_cast<int>(dtype), ctx->props.gcnArchName, gemmConfig(r));
+  if (!r.tuned && repeat > 0) {
+    LC_TRY(settleVariant(ctx, r));
+    r.tuned = true;
   }
   for (std::size_t i = 0; i < repeat; ++i) {
     traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, hint);
-    const hipError_t e = launchGemm(ctx, r);
+    const hipError_t e = launchGemm(ctx, r, r.variant);
     if (e != hipSuccess) {
       return failHip(e, "matmul kernel launch");
     }

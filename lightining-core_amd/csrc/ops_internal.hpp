@@ -32,6 +32,7 @@ struct AttnResident {
   AttnShape shape;
   DeviceBuffer q, k, v, out, stage;
   DeviceBuffer target, stats, loss;
+  DeviceBuffer v_scratch;  // the train step's dV autotune runs on a copy of V
   bool has_q = false, has_k = false, has_v = false, has_out = false, has_target = false;
 };
 
@@ -58,6 +59,11 @@ struct MatMulResident {
   lcDataType dtype = LC_DTYPE_F32;
   DeviceBuffer a, b, c, stage;
   bool has_a = false, has_b = false, has_c = false;
+  // GEMM kernel variant for this shape (kern::GemmF32Variant or
+  // kern::GemmHalfVariant as int; 0 = the launcher's own choice), settled on
+  // the first launch from the tune cache, an autotune or the heuristic.
+  int variant = 0;
+  bool tuned = false;
 };
 
 Status matmulResident(HipContext* ctx, MatMulResident& res, std::size_t m, std::size_t k, std::size_t n,

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "lc_internal.hpp"
+#include "tune.hpp"
 
 namespace lchip {
 
@@ -141,6 +142,7 @@ void initContext() {
 }  // namespace
 
 HipContext* hipContext(Status* st) {
+  ensureRuntimeProfileLoaded();
   std::call_once(g_ctx_once, initContext);
   if (g_ctx == nullptr) {
     if (st != nullptr) {

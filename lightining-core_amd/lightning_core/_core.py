@@ -17,7 +17,9 @@ __all__ = [
     "runtime_backend_capabilities", "runtime_backend_interface_contract", "backend_name", "is_hip_available",
     "is_cuda_available", "is_metal_available", "device_info", "api_version", "runtime_trace_enable",
     "runtime_trace_clear", "runtime_trace_events", "runtime_trace_event_capacity", "decode_dispatch_detail",
-    "tune_cache_save", "tune_cache_load", "device_synchronize", "LightningCoreError",
+    "tune_cache_save", "tune_cache_load", "tune_cache_size", "attention_tune_cache_save",
+    "attention_tune_cache_load", "attention_reset_tuning", "attention_tune_cache_size",
+    "preload_runtime_profile_env", "device_synchronize", "LightningCoreError",
 ]
 
 _DEVICES = {"cpu": N.LC_DEVICE_CPU, "cuda": N.LC_DEVICE_CUDA, "metal": N.LC_DEVICE_METAL, "hip": N.LC_DEVICE_HIP}
@@ -731,11 +733,39 @@ def runtime_trace_events() -> list:
 
 
 def tune_cache_save(path: str):
+    """Writes the gfx950 matmul tune cache (#lc_tune_cache,matmul,2)."""
     _check(_lib().lcHipTuneCacheSave(path.encode()))
 
 
 def tune_cache_load(path: str):
+    """Reads a matmul tune cache (versions 1-2) and makes it the cache file."""
     _check(_lib().lcHipTuneCacheLoad(path.encode()))
+
+
+def tune_cache_size() -> int:
+    return int(_lib().lcHipTuneCacheSize())
+
+
+def attention_tune_cache_save(path: str):
+    """Writes the attention tune cache (#lc_tune_cache,attention,2)."""
+    _check(_lib().lcHipAttentionTuneCacheSave(path.encode()))
+
+
+def attention_tune_cache_load(path: str):
+    _check(_lib().lcHipAttentionTuneCacheLoad(path.encode()))
+
+
+def attention_reset_tuning():
+    _check(_lib().lcHipAttentionResetTuning())
+
+
+def attention_tune_cache_size() -> int:
+    return int(_lib().lcHipAttentionTuneCacheSize())
+
+
+def preload_runtime_profile_env():
+    """runtime::preloadRuntimeProfileEnv (src/runtime.cpp:101-168, :421-423)."""
+    _lib().lcPreloadRuntimeProfileEnv()
 
 
 class HipTimer:

@@ -194,6 +194,12 @@ SIGNATURES = {
     "lcHipTimerStop": (_E, [c_void_p, P(c_float)]),
     "lcHipTuneCacheSave": (_E, [c_char_p]),
     "lcHipTuneCacheLoad": (_E, [c_char_p]),
+    "lcHipTuneCacheSize": (c_size, []),
+    "lcHipAttentionTuneCacheSave": (_E, [c_char_p]),
+    "lcHipAttentionTuneCacheLoad": (_E, [c_char_p]),
+    "lcHipAttentionResetTuning": (_E, []),
+    "lcHipAttentionTuneCacheSize": (c_size, []),
+    "lcPreloadRuntimeProfileEnv": (None, []),
 }
 
 _lib = None

@@ -1,0 +1,167 @@
+"""Tune caches on the hip device: first-call autotune, cache files, forced variants.
+
+Mirrors the reference's tests/test_python_tune_cache_format_smoke.py:35-88:
+v1-seeded cache files in the working directory are rewritten with the v2
+header and a "#columns," line once a new shape is tuned.  Then every GEMM
+variant and every attention split count is forced through a seeded cache on
+odd shapes and checked against float64 / the oracle: the autotuner may pick
+any of them.  Each case runs in a fresh interpreter (the caches are loaded
+once per process) with its own working directory.
+"""
+import json
+import os
+import subprocess
+import sys
+import textwrap
+
+import numpy as np
+import pytest
+
+from gpu_util import note, require_hip
+from lightning_core import synth
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "lightining-core_amd")
+TESTS = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def lc():
+    return require_hip()
+
+
+def _child(code, cwd, env=None):
+    e = {k: v for k, v in os.environ.items() if not k.startswith("CJ_")}
+    e.update(env or {})
+    e["PYTHONPATH"] = os.pathsep.join([PKG, TESTS, e.get("PYTHONPATH", "")])
+    note(f"[tune] child in {cwd} env={ {k: v for k, v in (env or {}).items()} }")
+    r = subprocess.run([sys.executable, "-u", "-c", textwrap.dedent(code)], cwd=cwd, env=e, capture_output=True,
+                       text=True, timeout=110)
+    note("\n".join(l for l in r.stdout.splitlines() if not l.startswith("OUT"))[-3000:])
+    assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
+    return r.stdout
+
+
+def _lines(path):
+    with open(path, encoding="utf-8") as f:
+        return [l.rstrip("\n") for l in f if l.strip()]
+
+
+def test_v1_seeded_caches_rewritten_after_autotune(lc, tmp_path):
+    (tmp_path / ".lightning_core_matmul_tune_cache.csv").write_text("#lc_tune_cache,matmul,1\n64,64,64,16,1,0\n")
+    (tmp_path / ".lightning_core_attn_tune_cache.csv").write_text("#lc_tune_cache,attention,1\nfwd,8,8,0,0,0,0\n")
+    _child("""
+        import numpy as np
+        import lightning_core as lc
+        rng = np.random.default_rng(7)
+        a = (rng.standard_normal((16, 16)) * 0.2).astype(np.float32)
+        b = (rng.standard_normal((16, 16)) * 0.2).astype(np.float32)
+        c = lc.matmul2d(a, b, device="hip")
+        assert np.abs(c - a.astype(np.float64) @ b).max() < 1e-5
+        q, k, v = ((rng.standard_normal((16, 16)) * 0.2).astype(np.float32) for _ in range(3))
+        o = np.asarray(lc.attention2d(q, k, v, causal=False, device="hip")).reshape(16, 16)
+        s = q.astype(np.float64) @ k.T / 4.0
+        p = np.exp(s - s.max(1, keepdims=True)); p /= p.sum(1, keepdims=True)
+        assert np.abs(o - p @ v).max() < 1e-5
+        # a 256 x 64 train step fills a T row (autotuned dV splits)
+        sess = lc.AttentionSession(256, 64, causal=True)
+        q, k, v, t = ((rng.standard_normal((256, 64))).astype(np.float32) for _ in range(4))
+        sess.train_step(q, k, v, t, 0.5)
+        sess.close()
+        print("ok")
+    """, tmp_path)
+    mm = _lines(tmp_path / ".lightning_core_matmul_tune_cache.csv")
+    at = _lines(tmp_path / ".lightning_core_attn_tune_cache.csv")
+    note(f"[tune] matmul cache: {mm}")
+    note(f"[tune] attention cache: {at}")
+    assert mm[0] == "#lc_tune_cache,matmul,2" and mm[1].startswith("#columns,")
+    assert at[0] == "#lc_tune_cache,attention,2" and at[1].startswith("#columns,")
+    assert "64,64,64,16,1,0" in mm  # the reference-layout row is kept
+    assert any(r.startswith("16,16,16,0,gfx950,f32_") for r in mm)
+    assert any(r.startswith("F,16,16,0,") for r in at)
+    assert any(r.startswith("T,256,64,1,") for r in at)
+
+
+F32_CASES = [("f32_dp_64x64x64", (100, 130, 77)), ("f32_streamk_64x64x64", (257, 300, 64)),
+             ("f32_dp_64x64x32", (1000, 777, 1030)), ("f32_streamk_64x64x64", (1000, 777, 1030))]
+HALF_CASES = [("half_lds_256x256", (300, 129, 200)), ("half_big8_256x256", (300, 129, 200)),
+              ("half_big4_256x256", (520, 256, 130)), ("half_mid_128x128", (77, 320, 513)),
+              ("half_small_64x64", (1000, 777, 1030)), ("half_skinny_16x32", (9, 200, 300))]
+_TILES = {"f32_dp_64x64x64": "64,64,64,8,2", "f32_streamk_64x64x64": "64,64,64,8,2",
+          "f32_dp_64x64x32": "64,64,32,8,2", "half_lds_256x256": "256,256,64,8,1",
+          "half_big8_256x256": "256,256,64,8,1", "half_big4_256x256": "256,256,64,4,1",
+          "half_mid_128x128": "128,128,64,4,1", "half_small_64x64": "64,64,64,4,1",
+          "half_skinny_16x32": "16,32,32,4,4"}
+
+
+@pytest.mark.parametrize("dtype,cases", [("f32", F32_CASES), ("bf16", HALF_CASES), ("f16", HALF_CASES)])
+def test_forced_gemm_variants(lc, tmp_path, dtype, cases):
+    # one seeded cache per (variant, shape), loaded in turn by one child
+    code = {"f32": 0, "bf16": 1, "f16": 2}[dtype]
+    jobs = []
+    for name, (m, k, n) in cases:
+        cache = tmp_path / f"mm_{name}_{m}_{k}_{n}.csv"
+        cache.write_text("#lc_tune_cache,matmul,2\n" + f"{m},{k},{n},{code},gfx950,{name},{_TILES[name]}\n")
+        jobs.append((str(cache), name, m, k, n))
+    before = {j[0]: open(j[0]).read() for j in jobs}
+    out = _child(f"""
+        import numpy as np
+        import lightning_core as lc
+        from lightning_core import synth
+        for cache, name, m, k, n in {jobs!r}:
+            print("[case]", name, m, k, n, flush=True)
+            lc.tune_cache_load(cache)
+            a = synth.normal((m, k), stream=11)
+            b = synth.normal((k, n), stream=12)
+            sess = lc.MatMulResidentSession(m, k, n, compute_dtype={dtype!r})
+            c = np.zeros(m * n, np.float32)
+            sess.start_into(a, b, c)
+            sess.finish_into(out=c)
+            sess.close()
+            ar, br = synth.round_to(a, {dtype!r}), synth.round_to(b, {dtype!r})
+            ref = ar.astype(np.float64) @ br.astype(np.float64)
+            err = np.abs(c.reshape(m, n) - ref).max() / np.abs(ref).max()
+            print("ERR", name, err, flush=True)
+    """, tmp_path)
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    errs = [l.split() for l in out.splitlines() if l.startswith("ERR")]
+    assert len(errs) == len(jobs)
+    for _, name, err in errs:
+        note(f"[parity] forced {name} {dtype} normwise={float(err):.3e}")
+        assert float(err) <= tol, name
+    for path, text in before.items():
+        assert open(path).read() == text  # the cached entry was used, not re-tuned
+
+
+@pytest.mark.parametrize("s,d,causal", [(256, 64, False), (200, 48, True), (130, 96, False)])
+def test_forced_attention_splits(lc, oracle, tmp_path, s, d, causal):
+    caches = []
+    for ks in (1, 2, 4, 8):
+        cache = tmp_path / f"attn_{ks}.csv"
+        cache.write_text("#lc_tune_cache,attention,2\n" + f"F,{s},{d},{int(causal)},0,0,{ks}\n"
+                         + f"F,{s},{d},{int(causal)},0,1,{ks}\n")
+        caches.append((ks, str(cache)))
+    out = _child(f"""
+        import json
+        import numpy as np
+        import lightning_core as lc
+        from lightning_core import synth
+        q, k, v = (synth.normal(({s}, {d}), stream=60 + i) for i in range(3))
+        for ks, cache in {caches!r}:
+            print("[case] splits", ks, flush=True)
+            lc.attention_tune_cache_load(cache)
+            o = np.asarray(lc.attention2d(q, k, v, causal={causal}, device="hip"))
+            print("OUT", ks, json.dumps(o.ravel().tolist()), flush=True)
+    """, tmp_path)
+    q, k, v = (synth.normal((s, d), stream=60 + i) for i in range(3))
+    ref = np.asarray(oracle.attention(q, k, v, causal)).ravel()
+    outs = [l for l in out.splitlines() if l.startswith("OUT")]
+    assert len(outs) == 4
+    for line in outs:
+        _, ks, payload = line.split(" ", 2)
+        got = np.asarray(json.loads(payload), np.float32)
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        note(f"[parity] forced attention splits={ks} S={s} D={d} causal={causal} normwise={err:.3e}")
+        assert err <= 1e-4

@@ -165,5 +165,5 @@ def test_tune_cache_header_roundtrip(tmp_path):
     lc.tune_cache_save(str(p))
     assert "64,64,64,1,gfx950,half_tn_32x32x16,128,128,64,4,1" in p.read_text()
     p.write_text("#lc_tune_cache,attention,9\n")
-    with pytest.raises(RuntimeError, match="bad header"):
+    with pytest.raises(RuntimeError, match="unsupported header"):
         lc.tune_cache_load(str(p))
