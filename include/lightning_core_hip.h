@@ -381,6 +381,19 @@ lcError_t lcConvAttentionTorchstrongNchw(const float* x, const float* w, const f
                                          size_t head_dim, size_t stride_h, size_t stride_w, size_t pad_h,
                                          size_t pad_w, lcDeviceKind device);
 
+/* The same call in graph mode (convAttentionTorchstrongNchwIntoGraph,
+ * bind_integrated.cpp:745-837): 3x3 weights only (else LC_NOT_SUPPORTED with
+ * the reference's message); one plan per key (geometry, seq_len, head_dim,
+ * has_bias), here a HIP graph captured on the first call and replayed after.
+ * Results equal the eager call's.  Clear drops every plan (syncs first). */
+lcError_t lcConvAttentionTorchstrongNchwGraph(const float* x, const float* w, const float* bias, float* out,
+                                              size_t batch, size_t in_channels, size_t in_h, size_t in_w,
+                                              size_t out_channels, size_t kernel_h, size_t kernel_w, size_t seq_len,
+                                              size_t head_dim, size_t stride_h, size_t stride_w, size_t pad_h,
+                                              size_t pad_w, lcDeviceKind device);
+lcError_t lcConvAttentionGraphCacheClear(void);
+size_t lcConvAttentionGraphCacheSize(void);
+
 /* ViT-style block (new composition of the reference's conv2dNchw, matMul and
  * attentionForward): patch-embed conv (kernel = stride = patch, no padding,
  * no bias) + ReLU -> tokens [B, T, E] -> QKV = tokens . w_qkv [E, 3E] split in

@@ -18,6 +18,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <memory>
 #include <string>
 #include <tuple>
 
@@ -100,6 +101,153 @@ Status convForwardDevice(HipContext* ctx, ConvResident& r, const ConvGeom& g, co
                               static_cast<int>(g.out_h * g.out_w), ctx->stream);
   }
   return e == hipSuccess ? Status::kSuccess : failHip(e, "conv2d kernel launch");
+}
+
+// ---------------------------------------------------------------------------
+// execution_mode="graph" (convAttentionTorchstrongNchwIntoGraph,
+// bind_integrated.cpp:745-837).  The reference plans a graph IR once per key
+// (ConvAttnGraphSessionKey: conv geometry, seq_len, head_dim, has_bias) and
+// executes it per call.  Here the plan is a HIP graph: the chain is captured
+// once per key and replayed with one hipGraphLaunch (a plan that is a single
+// kernel reading and writing mapped staging is launched directly: a one-node
+// graph only adds launch latency).  The session owns its device buffers and
+// pinned staging (captured pointers never move); inputs are packed into the
+// staging before each replay and the output is read from it after the stream
+// sync.  Nodes are kernels and copies only.
+// ---------------------------------------------------------------------------
+struct ConvAttnGraphSession {
+  ConvGeom g{};
+  std::size_t seq = 0, dim = 0, need = 0, xs = 0, ws = 0, bs = 0;
+  std::size_t w_at = 0, b_at = 0, in_floats = 0, out_at = 0;  // staging offsets in floats, 256-byte aligned
+  bool fused = false, mapped = false;
+  PinnedBuffer stage;
+  DeviceBuffer in, cols, conv_out, packed, attn_out;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  ConvAttnGraphSession() = default;
+  ConvAttnGraphSession(const ConvAttnGraphSession&) = delete;
+  ConvAttnGraphSession& operator=(const ConvAttnGraphSession&) = delete;
+  ~ConvAttnGraphSession() {
+    if (exec != nullptr) (void)hipGraphExecDestroy(exec);
+    if (graph != nullptr) (void)hipGraphDestroy(graph);
+  }
+};
+
+using GraphKey = std::tuple<std::size_t, std::size_t, std::size_t, std::size_t, std::size_t, std::size_t, std::size_t,
+                            std::size_t, std::size_t, std::size_t, std::size_t, std::size_t, std::size_t, bool>;
+
+std::map<GraphKey, std::unique_ptr<ConvAttnGraphSession>>& graphSessions() {
+  static auto* m = new std::map<GraphKey, std::unique_ptr<ConvAttnGraphSession>>();  // process lifetime
+  return *m;
+}
+
+// The chain a session's graph holds, enqueued on the stream being captured:
+// the fused one-launch kernel for conv outputs of at most 8192 values (reading
+// the staging's device alias when it stages its inputs in LDS), else im2col,
+// the conv GEMM (+bias, ReLU, NCHW), the QkvPackRepeat fill and attention.
+hipError_t enqueueConvAttn(HipContext* ctx, ConvAttnGraphSession& s) {
+  const ConvGeom& g = s.g;
+  float* host = static_cast<float*>(s.stage.get());
+  const int S = static_cast<int>(s.seq);
+  const int D = static_cast<int>(s.dim);
+  hipError_t e = hipSuccess;
+  const float* dx = nullptr;
+  if (s.mapped) {
+    dx = static_cast<const float*>(s.stage.device());
+  } else {
+    e = hipMemcpyAsync(s.in.get(), host, s.in_floats * sizeof(float), hipMemcpyHostToDevice, ctx->stream);
+    dx = s.in.as<float>();
+  }
+  const float* dw = dx + s.w_at;
+  const float* dbias = s.bs != 0 ? dx + s.b_at : nullptr;
+  float* dout = s.mapped ? static_cast<float*>(s.stage.device()) + s.out_at : s.attn_out.as<float>();
+  if (s.fused) {
+    if (e == hipSuccess) {
+      e = kern::convAttentionF32(dx, dw, dbias, static_cast<int>(g.batch), static_cast<int>(g.in_c),
+                                 static_cast<int>(g.in_h), static_cast<int>(g.in_w), static_cast<int>(g.out_c),
+                                 static_cast<int>(g.kh), static_cast<int>(g.kw), static_cast<int>(g.sh),
+                                 static_cast<int>(g.sw), static_cast<int>(g.ph), static_cast<int>(g.pw), S, D, dout,
+                                 ctx->stream);
+    }
+  } else {
+    if (e == hipSuccess) {
+      e = kern::im2colF32(dx, s.cols.as<float>(), static_cast<int>(g.batch), static_cast<int>(g.in_c),
+                          static_cast<int>(g.in_h), static_cast<int>(g.in_w), static_cast<int>(g.kh),
+                          static_cast<int>(g.kw), static_cast<int>(g.sh), static_cast<int>(g.sw),
+                          static_cast<int>(g.ph), static_cast<int>(g.pw), static_cast<int>(g.out_h),
+                          static_cast<int>(g.out_w), ctx->stream);
+    }
+    if (e == hipSuccess) {
+      e = kern::gemmF32ConvNchw(s.cols.as<float>(), dw, s.conv_out.as<float>(), static_cast<int>(g.rows()),
+                                static_cast<int>(g.out_c), static_cast<int>(g.kin()), dbias, 1,
+                                static_cast<int>(g.out_h * g.out_w), ctx->stream);
+    }
+    const float* src = s.conv_out.as<float>();
+    if (e == hipSuccess && g.outSize() < 3 * s.need) {
+      e = kern::repeatFillF32(s.conv_out.as<float>(), g.outSize(), s.packed.as<float>(), 3 * s.need, ctx->stream);
+      src = s.packed.as<float>();
+    }
+    if (e == hipSuccess) {
+      e = kern::attentionF32(src, src + s.need, src + 2 * s.need, dout, 1, S, D, false, 1.0f, 0.0f, 0, nullptr,
+                             ctx->stream);
+    }
+  }
+  if (e == hipSuccess && !s.mapped) {
+    e = hipMemcpyAsync(host + s.out_at, s.attn_out.get(), s.need * sizeof(float), hipMemcpyDeviceToHost,
+                       ctx->stream);
+  }
+  return e;
+}
+
+// Sizes a new session and captures its graph.
+Status planConvAttnGraph(HipContext* ctx, ConvAttnGraphSession& s, const ConvGeom& g, std::size_t seq,
+                         std::size_t dim, bool has_bias) {
+  s.g = g;
+  s.seq = seq;
+  s.dim = dim;
+  s.need = seq * dim;
+  s.xs = g.batch * g.in_c * g.in_h * g.in_w;
+  s.ws = g.out_c * g.kin();
+  s.bs = has_bias ? g.out_c : 0;
+  s.w_at = roundUp(s.xs, 64);
+  s.b_at = roundUp(s.w_at + s.ws, 64);
+  s.in_floats = s.b_at + s.bs;
+  s.out_at = roundUp(s.in_floats, 64);
+  s.fused = g.outSize() <= 8192 && 3 * s.need < (std::size_t{1} << 31);
+  s.mapped = s.fused && kern::convAttentionStagesInputs(
+                            static_cast<int>(g.batch), static_cast<int>(g.in_c), static_cast<int>(g.in_h),
+                            static_cast<int>(g.in_w), static_cast<int>(g.out_c), static_cast<int>(g.kh),
+                            static_cast<int>(g.kw), static_cast<int>(g.sh), static_cast<int>(g.sw),
+                            static_cast<int>(g.ph), static_cast<int>(g.pw));
+  LC_TRY(s.stage.ensure((s.out_at + s.need) * sizeof(float)));
+  if (!s.mapped) {
+    LC_TRY(s.in.ensure(s.in_floats * sizeof(float)));
+    LC_TRY(s.attn_out.ensure(s.need * sizeof(float)));
+  }
+  if (!s.fused) {
+    LC_TRY(s.cols.ensure(g.rows() * g.kin() * sizeof(float)));
+    LC_TRY(s.conv_out.ensure(g.outSize() * sizeof(float)));
+    if (g.outSize() < 3 * s.need) {
+      LC_TRY(s.packed.ensure(3 * s.need * sizeof(float)));
+    }
+  }
+  if (s.fused && s.mapped) {
+    return Status::kSuccess;  // one kernel, no copies: launched directly (a one-node graph only adds latency)
+  }
+  // DeviceBuffer::ensure allocates synchronously: nothing below
+  // allocates, so the capture holds only this chain.
+  LC_HIP_TRY(hipStreamSynchronize(ctx->stream));
+  LC_HIP_TRY(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+  const hipError_t e = enqueueConvAttn(ctx, s);
+  hipGraph_t graph = nullptr;
+  const hipError_t end = hipStreamEndCapture(ctx->stream, &graph);  // always leave capture mode
+  if (e != hipSuccess || end != hipSuccess) {
+    if (graph != nullptr) (void)hipGraphDestroy(graph);
+    return failHip(e != hipSuccess ? e : end, "conv_attention graph capture");
+  }
+  s.graph = graph;
+  LC_HIP_TRY(hipGraphInstantiate(&s.exec, graph, nullptr, nullptr, 0));
+  return Status::kSuccess;
 }
 
 }  // namespace
@@ -349,6 +497,79 @@ lcError_t lcConvAttentionTorchstrongNchw(const float* x, const float* w, const f
   }
   return toLc(st);
 }
+
+lcError_t lcConvAttentionTorchstrongNchwGraph(const float* x, const float* w, const float* bias, float* out,
+                                              size_t batch, size_t in_channels, size_t in_h, size_t in_w,
+                                              size_t out_channels, size_t kernel_h, size_t kernel_w, size_t seq_len,
+                                              size_t head_dim, size_t stride_h, size_t stride_w, size_t pad_h,
+                                              size_t pad_w, lcDeviceKind device) {
+  if (x == nullptr || w == nullptr || out == nullptr || seq_len == 0 || head_dim == 0) {
+    return toLc(fail(Status::kInvalidValue, "conv_attention graph: null pointer or zero seq_len/head_dim"));
+  }
+  if (kernel_h != 3 || kernel_w != 3) {
+    return toLc(fail(Status::kNotSupported, "graph mode currently supports 3x3 conv weights"));
+  }
+  if (head_dim > 256) {
+    return toLc(fail(Status::kNotSupported, "conv_attention graph: head_dim <= 256"));
+  }
+  ConvGeom g{};
+  Status st = makeGeom(batch, in_channels, in_h, in_w, out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                       pad_w, &g);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  HipContext* ctx = nullptr;
+  st = requireHip(device, "conv_attention graph", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  const GraphKey key{batch, in_channels, in_h, in_w, out_channels, kernel_h, kernel_w, stride_h, stride_w, pad_h,
+                     pad_w, seq_len, head_dim, bias != nullptr};
+  auto& sessions = graphSessions();
+  auto it = sessions.find(key);
+  if (it == sessions.end()) {
+    auto fresh = std::make_unique<ConvAttnGraphSession>();
+    st = planConvAttnGraph(ctx, *fresh, g, seq_len, head_dim, bias != nullptr);
+    if (st != Status::kSuccess) {
+      return toLc(st);
+    }
+    it = sessions.emplace(key, std::move(fresh)).first;
+  }
+  ConvAttnGraphSession& s = *it->second;
+  float* stage = static_cast<float*>(s.stage.get());
+  std::memcpy(stage, x, s.xs * sizeof(float));
+  std::memcpy(stage + s.w_at, w, s.ws * sizeof(float));
+  if (s.bs != 0) {
+    std::memcpy(stage + s.b_at, bias, s.bs * sizeof(float));
+  }
+  traceOpDispatch(TraceOp::kConv2dNchw, Device::kHIP, Device::kHIP, false, g.rows() * g.out_c * g.kin());
+  traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, seq_len * seq_len * head_dim);
+  const hipError_t e = s.exec != nullptr ? hipGraphLaunch(s.exec, ctx->stream) : enqueueConvAttn(ctx, s);
+  if (e != hipSuccess) {
+    return toLc(failHip(e, "conv_attention graph launch"));
+  }
+  st = syncStream(ctx);
+  if (st == Status::kSuccess) {
+    std::memcpy(out, stage + s.out_at, s.need * sizeof(float));
+  }
+  return toLc(st);
+}
+
+lcError_t lcConvAttentionGraphCacheClear(void) {
+  Status st = Status::kSuccess;
+  HipContext* ctx = hipContext(&st);
+  if (ctx != nullptr) {
+    std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+    (void)hipStreamSynchronize(ctx->stream);
+    graphSessions().clear();
+  } else {
+    graphSessions().clear();
+  }
+  return LC_SUCCESS;
+}
+
+size_t lcConvAttentionGraphCacheSize(void) { return graphSessions().size(); }
 
 lcError_t lcVitBlockSessionCreate(const lcVitBlockConfig* cfg, lcDeviceKind device, lcVitBlockSession** out) {
   if (cfg == nullptr || out == nullptr) {

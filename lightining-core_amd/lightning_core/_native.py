@@ -181,6 +181,9 @@ SIGNATURES = {
     "lcMatMulResidentSessionRunBatchSyncCachedNoDownload": (_E, [c_void_p, c_size]),
     "lcConv2dNchw": (_E, [BUF, BUF, BUF, BUF] + [c_size] * 11 + [c_int, c_int]),
     "lcConvAttentionTorchstrongNchw": (_E, [BUF, BUF, BUF, BUF] + [c_size] * 13 + [c_int]),
+    "lcConvAttentionTorchstrongNchwGraph": (_E, [BUF, BUF, BUF, BUF] + [c_size] * 13 + [c_int]),
+    "lcConvAttentionGraphCacheClear": (_E, []),
+    "lcConvAttentionGraphCacheSize": (c_size, []),
     "lcVitBlockSessionCreate": (_E, [P(VitBlockConfig), c_int, P(c_void_p)]),
     "lcVitBlockSessionDestroy": (_E, [c_void_p]),
     "lcVitBlockSessionSetWeights": (_E, [c_void_p, BUF, BUF, BUF]),

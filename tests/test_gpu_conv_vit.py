@@ -78,6 +78,59 @@ def test_conv_attention_shapes(lc, oracle, xs, ws, stride, pad, seq, hd):
     assert_parity(ref.ravel(), got, "f32", f"conv_attention {xs} {ws} seq={seq} d={hd}")
 
 
+# Graph mode: one HIP graph per shape key, replayed.  Each case replays it four
+# times with fresh inputs, an eager call (and its stream sync) between the
+# replays, and checks every replay bit for bit against the eager result (same
+# kernels, same arithmetic), plus the oracle once.  Shapes: the fused kernel
+# reading mapped staging, the fused kernel with an input too large to stage
+# (device copies in the graph), and the unfused im2col / GEMM / repeat chain.
+@pytest.mark.parametrize("xs,ws,stride,pad,seq,hd,with_bias", [
+    ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 48, 48, True),
+    ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 192, 8, False),
+    ((1, 4, 64, 64), (8, 4, 3, 3), (4, 4), (1, 1), 64, 32, True),
+    ((2, 3, 33, 31), (16, 3, 3, 3), (1, 1), (1, 1), 100, 64, True),
+    ((1, 3, 40, 40), (24, 3, 3, 3), (1, 1), (1, 1), 64, 200, False),
+])
+def test_conv_attention_graph_replays(lc, oracle, xs, ws, stride, pad, seq, hd, with_bias):
+    for it in range(4):
+        x, w = synth.normal(xs, stream=600 + it), synth.normal(ws, std=0.3, stream=610 + it)
+        bias = synth.normal((ws[0],), stream=620 + it) if with_bias else None
+        note(f"[graph] {xs} {ws} seq={seq} d={hd} bias={with_bias} replay {it}")
+        g = lc.api.conv_attention_torchstrong_nchw(x, w, bias, seq, hd, stride[0], stride[1], pad[0], pad[1],
+                                                   execution_mode="graph")
+        e = lc.api.conv_attention_torchstrong_nchw(x, w, bias, seq, hd, stride[0], stride[1], pad[0], pad[1],
+                                                   execution_mode="eager")
+        np.testing.assert_array_equal(g, e)
+        if it == 0:
+            ref = oracle.conv_attention(x, w, bias, seq, hd, stride, pad)
+            assert_parity(ref.ravel(), g, "f32", f"graph conv_attention {xs} {ws} seq={seq} d={hd}")
+
+
+def test_conv_attention_graph_non3x3_fallback_and_strict(lc, monkeypatch):
+    x, w = synth.normal((1, 2, 9, 11), stream=630), synth.normal((5, 2, 3, 2), std=0.3, stream=631)
+    e = lc.api.conv_attention_torchstrong_nchw(x, w, None, 30, 7, 2, 1, 0, 0, execution_mode="eager")
+    monkeypatch.delenv("LC_GRAPH_MODE_STRICT", raising=False)
+    g = lc.api.conv_attention_torchstrong_nchw(x, w, None, 30, 7, 2, 1, 0, 0, execution_mode="graph")
+    np.testing.assert_array_equal(g, e)  # the reference's fallback contract: the eager result
+    monkeypatch.setenv("LC_GRAPH_MODE_STRICT", "1")
+    with pytest.raises(RuntimeError, match="3x3 conv weights"):
+        lc.api.conv_attention_torchstrong_nchw(x, w, None, 30, 7, 2, 1, 0, 0, execution_mode="graph")
+
+
+def test_conv_attention_ab_report_and_cache(lc):
+    lc.api.clear_conv_attention_graph_cache()
+    assert lc._core._lib().lcConvAttentionGraphCacheSize() == 0
+    x, w = synth.normal((1, 3, 8, 8), stream=640), synth.normal((16, 3, 3, 3), std=0.3, stream=641)
+    b = synth.normal((16,), stream=642)
+    rep = lc.api.conv_attention_torchstrong_nchw_ab_report(x, w, b, 96, 48, 1, 1, 1, 1, warmup=2, repeat=10)
+    note(f"[graph] ab report {rep}")
+    assert rep["allclose"] and rep["max_abs_diff"] == 0.0
+    assert rep["winner"] in ("graph", "eager", "tie") and rep["eager_ms"] > 0 and rep["graph_ms"] > 0
+    assert lc._core._lib().lcConvAttentionGraphCacheSize() == 1
+    lc.api.clear_conv_attention_graph_cache()
+    assert lc._core._lib().lcConvAttentionGraphCacheSize() == 0
+
+
 def test_conv_attention_graph_mode_matches_eager(lc):
     x, w = synth.normal((1, 3, 8, 8), stream=4), synth.normal((8, 3, 3, 3), stream=5)
     e = lc.api.conv_attention_torchstrong_nchw(x, w, None, 16, 16, 1, 1, 1, 1, execution_mode="eager")
