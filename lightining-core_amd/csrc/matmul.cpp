@@ -148,7 +148,7 @@ hipError_t launchGemm(HipContext* ctx, MatMulResident& r, int variant) {
   if (!isHalf(r.dtype)) {
     const int kp = static_cast<int>(roundUp(r.k, kern::kF32GemmBK));
     const int np = static_cast<int>(roundUp(r.n, kern::kF32GemmBN));
-    // stream-K: one workgroup per CU at most (112 KB of LDS each)
+    // stream-K: one workgroup per CU (a whole-tile grid may hold two per CU)
     const int groups = ctx->props.multiProcessorCount > 0 ? ctx->props.multiProcessorCount : 256;
     if (ctx->gemm_part.ensure(static_cast<std::size_t>(groups) * 4096 * sizeof(float)) != Status::kSuccess ||
         ctx->gemm_flags.ensure(static_cast<std::size_t>(groups) * sizeof(int), true) != Status::kSuccess) {
