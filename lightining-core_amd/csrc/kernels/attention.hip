@@ -276,24 +276,28 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
                                                                float scale, float post_scale, float post_bias,
                                                                int post_relu) {
   constexpr int DP = 32 * DT;
-  constexpr int KV = 32 * (DP + 1) + 32 * DP;  // floats of one wave's K + V tile
+  // Q and K rows have stride DP + 4: 16-byte aligned (float4 reads), and a
+  // 16-lane pass of one float4 per row touches 16 distinct bank groups.
+  constexpr int QKS = DP + 4;
+  constexpr int KV = 32 * QKS + 32 * DP;  // floats of one wave's K + V tile
   static_assert(!VEC || Src::kVec, "vector prefetch needs a global source");
-  __shared__ float Qs[32][DP + 1];
+  __shared__ __attribute__((aligned(16))) float Qs[32][QKS];
   __shared__ __attribute__((aligned(16))) float kv[KS][KV];
   __shared__ float srcbuf[Src::kLds > 0 ? Src::kLds : 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  float (*Ks)[DP + 1] = reinterpret_cast<float (*)[DP + 1]>(&kv[wave][0]);
-  float (*Vs)[DP] = reinterpret_cast<float (*)[DP]>(&kv[wave][32 * (DP + 1)]);
+  float (*Ks)[QKS] = reinterpret_cast<float (*)[QKS]>(&kv[wave][0]);
+  float (*Vs)[DP] = reinterpret_cast<float (*)[DP]>(&kv[wave][32 * QKS]);
+  // Workgroup qb: query block qb; its waves take the 32-key tiles w + KS n.
+  // Heaviest (causal) blocks first.
   const int nqb = (S + 31) / 32;
-  const int qb = nqb - 1 - static_cast<int>(blockIdx.x);  // heaviest (causal) blocks first
+  const int qb = nqb - 1 - static_cast<int>(blockIdx.x);
   const int q0 = qb * 32;
+  const int jfirst = wave * 32;
+  const int jstep = 32 * KS;
   const size_t head = static_cast<size_t>(blockIdx.y) * S * D;
   out += head;
   src.prologue(srcbuf, 64 * KS);
-
-  fill_rows<DP, 1, 0, 0>(src, srcbuf, &Qs[0][0], DP + 1, nullptr, 0, wave, KS, q0, S, D, head, lane);
-  __syncthreads();
 
   floatx16 o[DT];
 #pragma unroll
@@ -326,40 +330,49 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
       }
     }
   };
+  // The first K / V tile's loads go out before the Q tile's, so their
+  // latencies overlap.
   if constexpr (VEC) {
-    if (wave * 32 < kend) {
-      fetch(wave * 32);
+    if (jfirst < kend) {
+      fetch(jfirst);
     }
   }
-  for (int j0 = wave * 32; j0 < kend; j0 += 32 * KS) {
+  fill_rows<DP, 1, 0, 0>(src, srcbuf, &Qs[0][0], QKS, nullptr, 0, wave, KS, q0, S, D, head, lane);
+  __syncthreads();
+  for (int j0 = jfirst; j0 < kend; j0 += jstep) {
     if constexpr (VEC) {
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int idx = c * 64 + lane;
         const int r = idx / (DP / 4);
         const int cc = (idx - r * (DP / 4)) * 4;
-        Ks[r][cc] = kr[c].x;
-        Ks[r][cc + 1] = kr[c].y;
-        Ks[r][cc + 2] = kr[c].z;
-        Ks[r][cc + 3] = kr[c].w;
+        *reinterpret_cast<float4*>(&Ks[r][cc]) = kr[c];
         *reinterpret_cast<float4*>(&Vs[r][cc]) = vr[c];
       }
-      if (j0 + 32 * KS < kend) {
-        fetch(j0 + 32 * KS);
+      if (j0 + jstep < kend) {
+        fetch(j0 + jstep);
       }
     } else {
-      fill_rows<DP, 2, 1, 2>(src, srcbuf, &Ks[0][0], DP + 1, &Vs[0][0], DP, 0, 1, j0, S, D, head, lane);
+      fill_rows<DP, 2, 1, 2>(src, srcbuf, &Ks[0][0], QKS, &Vs[0][0], DP, 0, 1, j0, S, D, head, lane);
     }
     __builtin_amdgcn_wave_barrier();
 
-    // Over the padded DP (columns D..DP-1 of both tiles are zero): a
-    // compile-time trip count lets the LDS reads run ahead of the MFMAs.
+    // Over the padded DP (columns D..DP-1 of both tiles are zero).  The k
+    // order inside the MFMAs is free as long as K and Q agree: lane half h
+    // takes k in [h DP/2, (h+1) DP/2), so each lane reads 4 k at a time.
     floatx16 st = zero16();
+    {
+      const float* krow = &Ks[lane & 31][(lane >> 5) * (DP / 2)];
+      const float* qrow = &Qs[lane & 31][(lane >> 5) * (DP / 2)];
 #pragma unroll
-    for (int dd = 0; dd < DP; dd += 2) {
-      const float a = Ks[lane & 31][dd + (lane >> 5)];
-      const float b = Qs[lane & 31][dd + (lane >> 5)];
-      st = mfma32x32x2f32(a, b, st);
+      for (int k4 = 0; k4 < DP / 2; k4 += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(krow + k4);
+        const float4 b4 = *reinterpret_cast<const float4*>(qrow + k4);
+        st = mfma32x32x2f32(a4.x, b4.x, st);
+        st = mfma32x32x2f32(a4.y, b4.y, st);
+        st = mfma32x32x2f32(a4.z, b4.z, st);
+        st = mfma32x32x2f32(a4.w, b4.w, st);
+      }
     }
     float mt = kMaskValue;
 #pragma unroll
@@ -406,12 +419,28 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
   }
 
   l_run += __shfl_xor(l_run, 32);
-  float inv = 1.0f / l_run;
-  float m_fin = m_run;
-  float l_fin = l_run;
-  if constexpr (KS > 1) {
+  // The normalised 32 x D output block is assembled in Qs' storage (free:
+  // every wave is past its QK^T) with row stride DP + 1, so writes by query
+  // are free of bank conflicts, and then stored as contiguous rows by every
+  // wave: full lines in HBM, and few large transactions when out is mapped
+  // host memory.
+  constexpr int TS = DP + 1;
+  float* tile = &Qs[0][0];
+  auto post = [&](float val) {
+    if (post_scale != 1.0f || post_bias != 0.0f || post_relu) {
+      val = val * post_scale + post_bias;
+      if (post_relu && val < 0.0f) {
+        val = 0.0f;
+      }
+    }
+    return val;
+  };
+  const int ql = lane & 31;
+  if (KS > 1) {
     // Park each wave's state in its own K / V region: m, l (32 each), then
-    // O^T as [d][query].  A wave that saw no key tile parks m = -1e30, l = 0.
+    // O^T as [query][d] (row stride DP + 1).  A wave that saw no key tile
+    // parks m = -1e30, l = 0.
+    constexpr int PS = DP + 1;
     float* mine = &kv[wave][0];
     if (lane < 32) {
       mine[lane] = m_run;
@@ -421,14 +450,12 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
     for (int t = 0; t < DT; ++t) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        mine[64 + (t * 32 + acc_row(i, lane)) * 32 + (lane & 31)] = o[t][i];
+        mine[64 + ql * PS + t * 32 + acc_row(i, lane)] = o[t][i];
       }
     }
     __syncthreads();
-    if (wave != 0) {
-      return;
-    }
-    const int ql = lane & 31;
+    // Every wave merges a share: lane (ql, half) of wave w takes the output
+    // columns d = 2 (w + KS n) + half of query ql.
     float m_all = kMaskValue;
 #pragma unroll
     for (int w = 0; w < KS; ++w) {
@@ -441,63 +468,50 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
       f[w] = exp2f(kv[w][ql] - m_all);
       l_all += f[w] * kv[w][32 + ql];
     }
-    inv = 1.0f / l_all;
-    m_fin = m_all;
-    l_fin = l_all;
+    const float inv = 1.0f / l_all;
+    // Row statistics for a later pass that recomputes P (the train
+    // step's dV): p = exp2(x - m) / l with x = (q.k) * scale * log2(e).
+    if (stats != nullptr && wave == 0 && lane < 32 && qi < S) {
+      stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2] = m_all;
+      stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2 + 1] = l_all;
+    }
+    for (int d = 2 * wave + (lane >> 5); d < D; d += 2 * KS) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int w = 0; w < KS; ++w) {
+        acc += f[w] * kv[w][64 + ql * PS + d];
+      }
+      tile[ql * TS + d] = post(acc * inv);
+    }
+  } else {
+    const float inv = 1.0f / l_run;
+    if (stats != nullptr && lane < 32 && qi < S) {
+      stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2] = m_run;
+      stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2 + 1] = l_run;
+    }
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int d = t * 32 + acc_row(i, lane);
-        float acc = 0.0f;
-#pragma unroll
-        for (int w = 0; w < KS; ++w) {
-          acc += f[w] * kv[w][64 + d * 32 + ql];
+        if (d < D) {
+          tile[ql * TS + d] = post(o[t][i] * inv);
         }
-        o[t][i] = acc;
       }
     }
   }
-  // Row statistics for a later pass that recomputes P (the train step's
-  // dV): p = exp2(x - m) / l with x = (q.k) * scale * log2(e).
-  if (stats != nullptr && lane < 32 && qi < S) {
-    stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2] = m_fin;
-    stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2 + 1] = l_fin;
-  }
-  // The 32 x D output block goes through Qs (free: every wave is past its
-  // QK^T) so that the stores cover contiguous rows: full lines in HBM, and
-  // few large transactions when out is mapped host memory.
-#pragma unroll
-  for (int t = 0; t < DT; ++t) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int d = t * 32 + acc_row(i, lane);
-      if (d < D) {
-        float val = o[t][i] * inv;
-        if (post_scale != 1.0f || post_bias != 0.0f || post_relu) {
-          val = val * post_scale + post_bias;
-          if (post_relu && val < 0.0f) {
-            val = 0.0f;
-          }
-        }
-        Qs[lane & 31][d] = val;
-      }
-    }
-  }
-  __builtin_amdgcn_wave_barrier();
-  const int total = min(32, S - q0) * D;
-  const int qstep = 64 / D;
-  const int cstep = 64 - qstep * D;
-  int r = lane / D;
-  int c = lane - r * D;
+  __syncthreads();
+  // Rows q0 .. q0 + rows - 1 are one contiguous range of out; wave w stores
+  // rows w, w + KS, ..., its lanes over the columns.
+  const int rows = min(32, S - q0);
   float* dst = out + static_cast<size_t>(q0) * D;
-  for (int idx = lane; idx < total; idx += 64) {
-    dst[idx] = Qs[r][c];
-    r += qstep;
-    c += cstep;
-    if (c >= D) {
-      c -= D;
-      ++r;
+  for (int r = wave; r < rows; r += KS) {
+#pragma unroll
+    for (int c0 = 0; c0 < DP; c0 += 64) {
+      const int c = c0 + lane;
+      if (c < D) {
+        dst[r * D + c] = tile[r * TS + c];
+      }
     }
   }
 }
@@ -1021,10 +1035,10 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
 #define LC_ATTN_F32(DT_, KS_)                                                                                       \
   if (vec && (DT_) <= 2) {                                                                                          \
     hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, ((DT_) <= 2), AttnSrcGlobal>), grid, dim3(64 * (KS_)), 0,    \
-                       stream, src, out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);                 \
+                       stream, src, out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);    \
   } else {                                                                                                          \
     hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false, AttnSrcGlobal>), grid, dim3(64 * (KS_)), 0, stream,   \
-                       src, out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);                         \
+                       src, out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);            \
   }
 #define LC_ATTN_F32_KS(DT_)                                                                                         \
   switch (ks) {                                                                                                     \
