@@ -552,7 +552,9 @@ constexpr int kHBK = 64;
 // staging registers and no LDS store instructions: the freed registers
 // double-buffer the MFMA fragments, so each k-step's LDS reads are issued
 // one step ahead of its MFMAs.  Stage k+1 is loaded while stage k is
-// computed; one wait + barrier per stage.
+// computed; one wait + barrier per stage.  The copies use a scalar tile base
+// and fixed 32-bit lane offsets (load_lds16_sbase): the host keeps
+// 256 * ld * 2 bytes below 2^31.
 // ---------------------------------------------------------------------------
 template <typename T, int WM, int WN, typename Epi>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uint16_t* __restrict__ A,
@@ -595,24 +597,29 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
   // chunk l%8, logical chunk (l%8) ^ ((row >> 1) & 7).
   const int lrow8 = lane >> 3;
   const int pchunk = lane & 7;
-  const uint16_t* a_src[LPW];
-  const uint16_t* b_src[LPW];
+  uint32_t a_off[LPW];  // byte offsets inside the tile's rows, fixed for all stages
+  uint32_t b_off[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int row = 8 * (NW * j + wave) + lrow8;
     const int lchunk = pchunk ^ ((row >> 1) & 7);
-    a_src[j] = A + static_cast<size_t>(bm + row) * lda + lchunk * 8;
-    b_src[j] = Bt + static_cast<size_t>(bn + row) * ldb + lchunk * 8;
+    a_off[j] = static_cast<uint32_t>(row * lda + lchunk * 8) * 2u;
+    b_off[j] = static_cast<uint32_t>(row * ldb + lchunk * 8) * 2u;
   }
+  const uint16_t* a_tile = A + static_cast<size_t>(bm) * lda;
+  const uint16_t* b_tile = Bt + static_cast<size_t>(bn) * ldb;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = lds_addr(smem);
   auto issue = [&](int buf, int k0) {
-    uint16_t* base = smem + buf * STAGE;
+    const uint32_t base = lds0 + 2u * static_cast<uint32_t>(buf * STAGE);
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      load_lds16(a_src[j] + k0, base + (NW * j + wave) * 8 * BK);
+      load_lds16_sbase(a_off[j], a_tile + k0, base + 2u * static_cast<uint32_t>((NW * j + wave_s) * 8 * BK));
     }
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      load_lds16(b_src[j] + k0, base + BM * BK + (NW * j + wave) * 8 * BK);
+      load_lds16_sbase(b_off[j], b_tile + k0,
+                       base + 2u * static_cast<uint32_t>(BM * BK + (NW * j + wave_s) * 8 * BK));
     }
   };
 
@@ -637,6 +644,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
   issue(0, 0);
   __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0); expcnt / lgkmcnt left at their maxima
   __syncthreads();
+  // Only this wave's LDS reads may be outstanding at the loop head: a pending
+  // scalar load would make every LDS wait in the loop an lgkmcnt(0).
+  __builtin_amdgcn_s_waitcnt(0xc07f);
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
     if (kt + 1 < nk) {
@@ -798,32 +808,35 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
   };
 
   // Wave w issues A instructions w + NW*j (A_RPI rows each) and B
-  // instructions w + NW*j (4 k-rows of 256 bytes each), j < LPW; offsets
-  // within a tile.
-  const float* a_src[LPW];
-  const float* b_src[LPW];
+  // instructions w + NW*j (4 k-rows of 256 bytes each), j < LPW; byte
+  // offsets within a tile, fixed for all stages (the host keeps
+  // 64 * ld * 4 bytes below 2^31).
+  uint32_t a_off[LPW];
+  uint32_t b_off[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int ins = wave + NW * j;
     const int row = A_RPI * ins + lane / ACH;
     const int lch = (lane % ACH) ^ swz(row);
-    a_src[j] = A + static_cast<size_t>(row) * lda + lch * 4;
+    a_off[j] = static_cast<uint32_t>(row * lda + lch * 4) * 4u;
     const int krow = 4 * ins + (lane >> 4);
-    b_src[j] = B + static_cast<size_t>(krow) * ldb + ((lane & 15) ^ (krow & 4 ? 8 : 0)) * 4;
+    b_off[j] = static_cast<uint32_t>(krow * ldb + ((lane & 15) ^ (krow & 4 ? 8 : 0)) * 4) * 4u;
   }
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = lds_addr(smem);
   // Issue cursor: next (tile, k) to load, walking down from it1 - 1.
   int is_t = (it1 - 1) / nk;
   int is_k = (it1 - 1) - is_t * nk;
   int is_bm, is_bn;
   origin(is_t, is_bm, is_bn);
   auto issue_next = [&](int buf) {
-    float* base = smem + buf * STAGE;
-    const size_t aoff = static_cast<size_t>(is_bm) * lda + is_k * BK;
-    const size_t boff = static_cast<size_t>(is_k) * BK * ldb + is_bn;
+    const uint32_t base = lds0 + 4u * static_cast<uint32_t>(buf * STAGE);
+    const float* a_base = A + static_cast<size_t>(is_bm) * lda + is_k * BK;
+    const float* b_base = B + static_cast<size_t>(is_k) * BK * ldb + is_bn;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      load_lds16(a_src[j] + aoff, base + (wave + NW * j) * 256);
-      load_lds16(b_src[j] + boff, base + A_STAGE + (wave + NW * j) * 256);
+      load_lds16_sbase(a_off[j], a_base, base + 4u * static_cast<uint32_t>((wave_s + NW * j) * 256));
+      load_lds16_sbase(b_off[j], b_base, base + 4u * static_cast<uint32_t>(A_STAGE + (wave_s + NW * j) * 256));
     }
     if (--is_k < 0) {
       is_k = nk - 1;
@@ -1103,6 +1116,10 @@ hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N,
   if (K <= 0 || K % kF32GemmBK != 0 || lda % 4 != 0 || ldb % 4 != 0 || M <= 0 || N <= 0 || max_groups <= 0) {
     return hipErrorInvalidValue;
   }
+  if (64LL * lda * 4 >= (1LL << 31) || 64LL * ldb * 4 >= (1LL << 31)) {
+    // beyond the LDS kernel's 32-bit lane offsets (64 rows of either operand)
+    return launch_gemm_f32<false>(A, B, M, N, K, lda, ldb, EpiStoreF32{C, ldc}, stream);
+  }
   const int tiles_m = (M + 63) / 64;
   const int tiles_n = (N + 63) / 64;
   if (variant == GemmF32Variant::kAuto) {
@@ -1161,7 +1178,12 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
   if (variant == GemmHalfVariant::kSkinny && M > 16) {
     return hipErrorInvalidValue;  // the skinny kernel holds at most 16 rows of A
   }
-  // A and Bt come from the resident upload, padded to 256 rows.
+  // A and Bt come from the resident upload, padded to 256 rows; the copies'
+  // 32-bit lane offsets reach 256 rows of either operand.
+  if (variant == GemmHalfVariant::kLds &&
+      (256LL * lda * 2 >= (1LL << 31) || 256LL * ldb * 2 >= (1LL << 31))) {
+    variant = GemmHalfVariant::kBig8;
+  }
   if (variant == GemmHalfVariant::kLds && K > 0) {
     return t == Half::kBF16 ? launch_gemm_lds<BF16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
                             : launch_gemm_lds<F16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);

@@ -102,6 +102,28 @@ __device__ __forceinline__ void load_lds16(const float* src, float* lds_base) {
   __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
 }
 
+// 16-byte global -> LDS copy of one lane from a wave-uniform base and a
+// 32-bit per-lane byte offset (LDS address = lds + 16*lane), written as
+// inline asm for two reasons:
+//  * the scalar-base form needs no per-lane 64-bit address: a tile's lane
+//    offsets are fixed, so a load costs one M0 move, and the wave issues the
+//    copy instead of a stream of 64-bit address adds (measured on the 8192^3
+//    bf16 GEMM: 1150 -> 1240 TFLOP/s);
+//  * the compiler's wait-count pass does not see it.  An outstanding
+//    compiler-visible global -> LDS copy makes every later LDS wait an
+//    lgkmcnt(0), which stalls each MFMA group on LDS reads issued for the
+//    next one.  Callers wait for these copies with explicit vmcnt.
+// `lds` and `sbase` must be wave-uniform; M0 is clobbered.
+__device__ __forceinline__ void load_lds16_sbase(uint32_t voff, const void* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
+               : "memory", "m0");
+}
+
+// LDS byte address of a __shared__ object, as a wave-uniform value.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
+}
+
 // s_waitcnt vmcnt(n) (expcnt / lgkmcnt left at their maxima; vmcnt's low
 // four bits sit in bits 3:0 of the immediate, its high two in bits 15:14).
 template <int N>
