@@ -736,34 +736,36 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   // Load mapping: wave w issues instructions w + 4j (j < LPW) of each operand.
   // K instruction i fills rows K_RPI*i + lane / KCH, physical chunk lane % KCH;
   // V^T instruction i fills rows 8i + lane / 8, physical chunk lane % 8.
-  // Per-lane element offsets are 32-bit (a head is far below 2^31
-  // elements); the tile base is uniform, so the loads take the
-  // scalar-base + vector-offset form and the offsets cost one VGPR each.
+  // Per-lane byte offsets are 32-bit (the host keeps a head below 2^30
+  // elements) and fixed; the tile base is uniform, so every copy takes the
+  // scalar-base form (load_lds16_sbase) with one M0 move of setup.
   const uint16_t* Kh = K + hoff;
   const uint16_t* Vh = Vt + hoff;
-  int k_off[LPW];
-  int v_off[LPW];
+  uint32_t k_off[LPW];
+  uint32_t v_off[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int ins = wave + 4 * j;
     const int kr = K_RPI * ins + lane / KCH;
     const int kswz = KCH == 16 ? (kr & 15) : ((kr >> 1) & 7);
-    k_off[j] = kr * D + ((lane % KCH) ^ kswz) * 8;
+    k_off[j] = static_cast<uint32_t>(kr * D + ((lane % KCH) ^ kswz) * 8) * 2u;
     const int vr = 8 * ins + (lane >> 3);
-    v_off[j] = vr * S_pad + ((lane & 7) ^ ((vr >> 1) & 7)) * 8;
+    v_off[j] = static_cast<uint32_t>(vr * S_pad + ((lane & 7) ^ ((vr >> 1) & 7)) * 8) * 2u;
   }
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = lds_addr(smem);
   auto issue_k = [&](int buf, int tile) {
     const uint16_t* base = Kh + static_cast<size_t>(tile) * KT * D;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      load_lds16(base + k_off[j], smem + buf * TILE + (wave + 4 * j) * 512);
+      load_lds16_sbase(k_off[j], base, lds0 + 2u * static_cast<uint32_t>(buf * TILE + (wave_s + 4 * j) * 512));
     }
   };
   auto issue_v = [&](int buf, int tile) {
     const uint16_t* base = Vh + tile * KT;
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      load_lds16(base + v_off[j], smem + (2 + buf) * TILE + (wave + 4 * j) * 512);
+      load_lds16_sbase(v_off[j], base, lds0 + 2u * static_cast<uint32_t>((2 + buf) * TILE + (wave_s + 4 * j) * 512));
     }
   };
 
@@ -1171,7 +1173,9 @@ hipError_t mseLossF32(const float* out, const float* target, size_t n, float nor
 hipError_t attentionHalf(const uint16_t* q, const uint16_t* k, const uint16_t* vt, float* out_f32,
                          uint16_t* out_heads_concat, int heads, int bh, int S, int S_pad, int D, bool causal, Half t,
                          hipStream_t stream) {
-  if (S <= 0 || bh <= 0 || S_pad % 128 != 0 || S_pad < S || (D != 64 && D != 128)) {
+  // The K / V^T copies use 32-bit byte offsets inside one head.
+  if (S <= 0 || bh <= 0 || S_pad % 128 != 0 || S_pad < S || (D != 64 && D != 128) ||
+      static_cast<long long>(S_pad) * D * 2 >= (1LL << 31)) {
     return hipErrorInvalidValue;
   }
   const float scale = 1.0f / sqrtf(static_cast<float>(D));

@@ -951,6 +951,9 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
   int ct = (it1 - 1) / nk;
   int ck = (it1 - 1) - ct * nk;
   bool seg_has_last = ck == nk - 1;
+  // Only LDS reads may be outstanding in the loop: a pending scalar load
+  // would make every fragment wait an lgkmcnt(0).
+  __builtin_amdgcn_s_waitcnt(0xc07f);
   for (int j = 0; j < n_it; ++j) {
     // Stage j's loads (own) have landed once at most min(n_it-1-j, STAGES-2)
     // later stages are outstanding; the barrier extends that to every wave
