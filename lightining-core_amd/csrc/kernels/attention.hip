@@ -838,7 +838,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
         mt = fmaxf(mt, s_cur[kt][i]);
       }
     }
-    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    mt = max_xor32(mt);
     // Rescale O and l only when some lane's max grew by more than 8 (exp2
     // units); otherwise keep the stale reference max.  O and l always share
     // the same reference, so O/l is unchanged; exponents stay <= 8.
@@ -871,29 +871,31 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
       const int s = g - kt * QS;
       return *reinterpret_cast<const u32x4*>(ksn + (kt * 32 + prow) * D + (((2 * s + half) ^ kswz) << 3));
     };
-    u32x4 kf0 = kfrag(0);
-    u32x4 kf1 = kfrag(1);
+    // Fragments rotate through a 3-entry ring indexed by the unrolled g
+    // (no register copies).
+    u32x4 kf[3];
+    kf[0] = kfrag(0);
+    kf[1] = kfrag(1);
 #pragma unroll
     for (int g = 0; g < NQK; ++g) {
-      u32x4 kf2;
       if (g + 2 < NQK) {
-        kf2 = kfrag(g + 2);
+        kf[(g + 2) % 3] = kfrag(g + 2);
       }
       {
         const int kt = g / QS;
         const int s = g - kt * QS;
-        s_nxt[kt] = mfma32x32x16<T>(kf0, qf[s], s == 0 ? zero16() : s_nxt[kt]);
+        s_nxt[kt] = mfma32x32x16<T>(kf[g % 3], qf[s], s == 0 ? zero16() : s_nxt[kt]);
       }
 #pragma unroll
       for (int e = 0; e < EPM; e += 2) {
         const int idx = g * EPM + e;  // score element idx and idx + 1
         const float p0 = fast_exp2(__builtin_fmaf(s_cur[idx >> 4][idx & 15], c, -mc));
         const float p1 = fast_exp2(__builtin_fmaf(s_cur[idx >> 4][(idx & 15) + 1], c, -mc));
-        ls += p0 + p1;
-        pb[idx >> 3][(idx & 7) >> 1] = pack2<T>(p0, p1);
+        const uint32_t pair = pack2<T>(p0, p1);
+        // l sums the rounded probabilities the P.V MFMAs consume.
+        ls = add_pair<T>(pair, ls);
+        pb[idx >> 3][(idx & 7) >> 1] = pair;
       }
-      kf0 = kf1;
-      kf1 = kf2;
       __builtin_amdgcn_sched_barrier(0);
     }
     l_run += ls;
@@ -905,19 +907,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
       return *reinterpret_cast<const u32x4*>(vs + (t * 32 + lrow) * KT + (((2 * ks2 + half) ^ vswz) << 3));
     };
     constexpr int NPV = 4 * DT;
-    u32x4 vf0 = vfrag(0);
-    u32x4 vf1 = vfrag(1);
+    u32x4 vf[3];
+    vf[0] = vfrag(0);
+    vf[1] = vfrag(1);
 #pragma unroll
     for (int g = 0; g < NPV; ++g) {
-      u32x4 vf2;
       if (g + 2 < NPV) {
-        vf2 = vfrag(g + 2);
+        vf[(g + 2) % 3] = vfrag(g + 2);
       }
       const int ks2 = g / DT;
       const int t = g - ks2 * DT;
-      o[t] = mfma32x32x16<T>(vf0, pb[ks2], o[t]);
-      vf0 = vf1;
-      vf1 = vf2;
+      o[t] = mfma32x32x16<T>(vf[g % 3], pb[ks2], o[t]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };

@@ -63,6 +63,29 @@ __device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// acc + lo + hi of a packed 16-bit pair, in one fp32 dot-product
+// instruction (v_dot2c_f32_{bf16,f16} against (1, 1)).
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <typename T>
+__device__ __forceinline__ float add_pair(uint32_t pair, float acc);
+template <>
+__device__ __forceinline__ float add_pair<BF16>(uint32_t pair, float acc) {
+  const bf16x2 ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), ones, acc, false);
+}
+template <>
+__device__ __forceinline__ float add_pair<F16>(uint32_t pair, float acc) {
+  const f16x2 ones = {static_cast<_Float16>(1.0f), static_cast<_Float16>(1.0f)};
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), ones, acc, false);
+}
+
+// max over lanes l and l ^ 32 (v_permlane32_swap: no LDS round trip).
+__device__ __forceinline__ float max_xor32(float v) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__builtin_bit_cast(float, r[0]), __builtin_bit_cast(float, r[1]));
+}
+
 // 32x32x16 MFMA on 8 packed 16-bit values per lane (as four dwords).
 template <typename T>
 __device__ __forceinline__ floatx16 mfma32x32x16(u32x4 a, u32x4 b, floatx16 c);
