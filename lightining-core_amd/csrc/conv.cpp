@@ -318,8 +318,8 @@ Status vitForwardDevice(HipContext* ctx, lcVitBlockSession* s) {
     return failHip(e, "vit attention launch");
   }
   traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, s->M * c.embed * c.embed);
-  e = kern::gemmHalfTN(s->attn16.as<uint16_t>(), s->wo_t16.as<uint16_t>(), s->out.as<float>(), M, E, E, E, E, E, ht,
-                       kern::GemmHalfVariant::kAuto, ctx->stream);
+  e = kern::outProjectGemm(s->attn16.as<uint16_t>(), s->wo_t16.as<uint16_t>(), s->out.as<float>(), M, E, ht,
+                           ctx->stream);
   return e == hipSuccess ? Status::kSuccess : failHip(e, "vit out-projection launch");
 }
 

@@ -126,6 +126,10 @@ hipError_t patchEmbedGemm(const uint16_t* x, const uint16_t* Wt, uint16_t* token
 // Vt [B*H, Dh, S_pad] (16-bit), M = B*T, S = T.
 hipError_t qkvProjectGemm(const uint16_t* tokens, const uint16_t* Wqkv_t, uint16_t* q, uint16_t* k, uint16_t* vt,
                           int B, int T, int E, int H, int S_pad, Half t, hipStream_t stream);
+// ViT output projection: out[M, E] (fp32) = attn[M, E] . Wo_t[E, E]^T (16-bit
+// operands, E % 64 == 0).
+hipError_t outProjectGemm(const uint16_t* attn, const uint16_t* Wo_t, float* out, int M, int E, Half t,
+                          hipStream_t stream);
 
 // Flash attention over `bh` problems: Q, K [bh, S_pad, D], Vt [bh, D, S_pad]
 // (16-bit, zero padded to S_pad = roundup(S, 128)), D in {64, 128}.  Output

@@ -282,6 +282,54 @@ struct EpiQKV {
       vt[(head * Dh + d) * S_pad + t] = bits;
     }
   }
+  // A whole 32x32 accumulator of one lane: column n (one head and d for the
+  // lane), rows mbase + 8g + 4*(lane/32) + i, i < 4, for g < 4.  Each group of
+  // 4 rows lies in one image when T_ % 4 == 0 (the caller checks), so its
+  // token index comes from one division and its 4 V^T values are one 8-byte
+  // store; Q and K rows stay 2-byte stores, 32 lanes to 64 contiguous bytes.
+  static constexpr bool kAccStore = true;
+  __device__ __forceinline__ void store_acc(int mbase, int n, const floatx16& acc, int lane, int M, int N) const {
+    if (n >= N) {
+      return;
+    }
+    const int which = n / E;
+    const int r = n - which * E;
+    const int h = r / Dh;
+    const int d = r - h * Dh;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int m0 = mbase + 8 * g + 4 * (lane >> 5);
+      if (m0 >= M) {
+        continue;
+      }
+      const int b = m0 / T_;
+      const int t0 = m0 - b * T_;
+      const size_t head = static_cast<size_t>(b) * H + h;
+      if (which == 2) {
+        u32x2 w;
+        w[0] = pack2<T>(acc[4 * g], acc[4 * g + 1]);
+        w[1] = pack2<T>(acc[4 * g + 2], acc[4 * g + 3]);
+        *reinterpret_cast<u32x2*>(vt + (head * Dh + d) * S_pad + t0) = w;
+      } else {
+        uint16_t* dst = (which == 0 ? q : k) + (head * S_pad + t0) * Dh + d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          dst[i * Dh] = to_half_bits<T>(acc[4 * g + i]);
+        }
+      }
+    }
+  }
+};
+
+// Whether an epilogue stores whole accumulators (store_acc) instead of
+// single elements.
+template <typename E, typename = void>
+struct AccStore {
+  static constexpr bool value = false;
+};
+template <typename E>
+struct AccStore<E, decltype(void(E::kAccStore))> {
+  static constexpr bool value = E::kAccStore;
 };
 
 template <typename T, int BM, int BN, int BK, int WM, int WN, int STORE_AT, typename LoadA, typename Epi>
@@ -711,6 +759,224 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
 }
 
 // ---------------------------------------------------------------------------
+// Ring-pipelined 16-bit TN GEMM for short K (the ViT block's GEMMs, K = 768).
+//
+// With K = 768 a tile has 12 stages of BK = 64 and each stage holds only a
+// few MFMAs per wave, so a loop that prefetches one stage ahead pays a global
+// load latency per stage.  Here NS stages of LDS form a ring and the copies of
+// stage s + NS - 1 go out when stage s starts: one latency per tile.
+// Copies are scalar-base global -> LDS (load_lds16_sbase) with the 128-byte
+// row swizzle of gemm_half_tn_lds_kernel; per-lane offsets are fixed for the
+// tile and rows past M (or N) are clamped to the last row (read, computed,
+// never stored).  The A source is a policy: row-major, or the implicit
+// im2col of a patch-embedding convolution.
+// ---------------------------------------------------------------------------
+
+// Row-major A [M, lda]: stage base = tile row bm, column k0.
+struct RingRowMajor {
+  const uint16_t* A;
+  int lda;
+  __device__ __forceinline__ const uint16_t* stage_base(int bm, int k0) const {
+    return A + static_cast<size_t>(bm) * lda + k0;
+  }
+  // Byte offset of (row, k0 + kk) from stage_base(bm, k0), row in [bm, M).
+  __device__ __forceinline__ uint32_t lane_offset(int bm, int row, int kk) const {
+    return static_cast<uint32_t>((row - bm) * lda + kk) * 2u;
+  }
+};
+
+// Implicit im2col of a patch-embedding convolution (kernel = stride = P, no
+// padding) over x [B, C, H, W]: row = b*T + ty*gw + tx, k = (c*P + ky)*P + kx.
+// With P dividing 64 and 64 dividing P*P a 64-wide stage is 64/P kernel rows
+// of one channel: k0 fixes (c, first ky) for every lane (the stage base) and
+// the lane adds its patch origin plus kk / P rows and kk % P columns.
+struct RingPatch {
+  const uint16_t* x;
+  int C, H, W, P, T, gw;
+  __device__ __forceinline__ const uint16_t* stage_base(int, int k0) const {
+    const int pp = P * P;
+    const int c = k0 / pp;
+    const int ky0 = (k0 - c * pp) / P;
+    return x + (static_cast<size_t>(c) * H + ky0) * W;
+  }
+  __device__ __forceinline__ uint32_t lane_offset(int, int row, int kk) const {
+    const int b = row / T;
+    const int t = row - b * T;
+    const int ty = t / gw;
+    const int tx = t - ty * gw;
+    const int origin = ((b * C) * H + ty * P) * W + tx * P;
+    return static_cast<uint32_t>(origin + (kk / P) * W + kk % P) * 2u;
+  }
+};
+
+template <typename T, int BM, int BN, int WM, int WN, int NS, typename ASrc, typename Epi>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, const uint16_t* __restrict__ Bt,
+                                                                       int M, int N, int K, int ldb, int tiles_n,
+                                                                       Epi epi) {
+  constexpr int BK = 64;
+  constexpr int NW = WM * WN;
+  constexpr int TM = BM / WM / 32;
+  constexpr int TN = BN / WN / 32;
+  constexpr int ROWB = BK * 2;                 // bytes per LDS row
+  constexpr int STAGE = (BM + BN) * BK;        // elements per stage
+  constexpr int A_INS = BM / 8;                // 1 KB copies of A per stage
+  constexpr int LPW = (BM + BN) / 8 / NW;      // copies per wave per stage
+  constexpr int A_LPW = A_INS / NW;            // ... of which A
+  static_assert(TM >= 1 && TN >= 1 && A_INS % NW == 0 && (BN / 8) % NW == 0, "tile / wave split");
+  static_assert(NS >= 2 && NS <= 5 && NS * STAGE * 2 <= 160 * 1024, "LDS ring");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[NS * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = (wave / WN) * (BM / WM);
+  const int wn = (wave % WN) * (BN / WN);
+
+  // XCD-aware grouped tile order (as gemm_half_tn_lds_kernel).
+  const int tiles_m = (M + BM - 1) / BM;
+  const int full = static_cast<int>(gridDim.x) & ~7;
+  int pid = blockIdx.x;
+  if (pid < full) {
+    pid = (pid & 7) * (full >> 3) + (pid >> 3);
+  }
+  const int group_size = 8 * tiles_n;
+  const int group = pid / group_size;
+  const int first_m = group * 8;
+  const int gm = min(tiles_m - first_m, 8);
+  const int in_group = pid - group * group_size;
+  const int bm = (first_m + in_group % gm) * BM;
+  const int bn = (in_group / gm) * BN;
+
+  // Copy j of this wave is instruction i = wave + NW*j: A rows 8i..8i+7 for
+  // j < A_LPW, else B rows 8(i - A_INS)..; lane l -> row + l/8, physical
+  // chunk l%8, logical chunk (l%8) ^ ((row >> 1) & 7).
+  uint32_t off[LPW];
+#pragma unroll
+  for (int j = 0; j < LPW; ++j) {
+    const int ins = wave + NW * j;
+    const int r = 8 * (j < A_LPW ? ins : ins - A_INS) + (lane >> 3);
+    const int kk = ((lane & 7) ^ ((r >> 1) & 7)) * 8;
+    if (j < A_LPW) {
+      off[j] = asrc.lane_offset(bm, min(bm + r, M - 1), kk);
+    } else {
+      off[j] = static_cast<uint32_t>((min(bn + r, N - 1) - bn) * ldb + kk) * 2u;
+    }
+  }
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = lds_addr(smem);
+  const uint16_t* b_tile = Bt + static_cast<size_t>(bn) * ldb;
+  auto issue = [&](int buf, int k0) {
+    const uint16_t* a_base = asrc.stage_base(bm, k0);
+#pragma unroll
+    for (int j = 0; j < LPW; ++j) {
+      const uint32_t dst = lds0 + 2u * static_cast<uint32_t>(buf * STAGE + (wave_s + NW * j) * 8 * BK);
+      load_lds16_sbase(off[j], j < A_LPW ? a_base : b_tile + k0, dst);
+    }
+  };
+
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  auto frag = [&](const uint16_t* base, int row, int c) -> u32x4 {
+    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + row * ROWB +
+                                           ((c ^ ((row >> 1) & 7)) << 4));
+  };
+  floatx16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      acc[i][j] = zero16();
+    }
+  }
+
+  const int nk = K / BK;
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s) {
+    if (s < nk) {
+      issue(s, s * BK);
+    }
+  }
+  // Only LDS reads may be outstanding in the loop (a pending scalar load
+  // would make every fragment wait an lgkmcnt(0)).
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  int buf = 0;
+  for (int kt = 0; kt < nk; ++kt) {
+    // Stage kt has landed (this wave's copies) once at most the later
+    // stages' copies are outstanding; the barrier extends that to every wave
+    // and retires everyone's reads of stage kt-1, whose buffer is refilled.
+    const int later = min(NS - 2, nk - 1 - kt);
+    if (later >= 3) {
+      wait_vmcnt<3 * LPW>();
+    } else if (later == 2) {
+      wait_vmcnt<2 * LPW>();
+    } else if (later == 1) {
+      wait_vmcnt<LPW>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    stage_barrier();
+    if (kt + NS - 1 < nk) {
+      issue(buf == 0 ? NS - 1 : buf - 1, (kt + NS - 1) * BK);
+    }
+    const uint16_t* As = smem + buf * STAGE;
+    const uint16_t* Bs = As + BM * BK;
+    u32x4 af[2][TM];
+    u32x4 bf[2][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      af[0][i] = frag(As, wm + i * 32 + lrow, lhalf);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      bf[0][j] = frag(Bs, wn + j * 32 + lrow, lhalf);
+    }
+#pragma unroll
+    for (int s = 0; s < BK / 16; ++s) {
+      const int cur = s & 1;
+      if (s + 1 < BK / 16) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) {
+          af[cur ^ 1][i] = frag(As, wm + i * 32 + lrow, 2 * (s + 1) + lhalf);
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          bf[cur ^ 1][j] = frag(Bs, wn + j * 32 + lrow, 2 * (s + 1) + lhalf);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          acc[i][j] = mfma32x32x16<T>(af[cur][i], bf[cur][j], acc[i][j]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    buf = buf + 1 == NS ? 0 : buf + 1;
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = bn + wn + j * 32 + lrow;
+      if constexpr (AccStore<Epi>::value) {
+        epi.store_acc(bm + wm + i * 32, n, acc[i][j], lane, M, N);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = bm + wm + i * 32 + acc_row(r, lane);
+          if (m < M && n < N) {
+            epi(m, n, acc[i][j][r]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 GEMM on padded operands: direct global -> LDS loads, stream-K.
 //
 // 64x64 block tile, 4*KS waves: each group of 4 waves covers the four 32x32
@@ -1080,6 +1346,25 @@ static hipError_t launch_gemm_half(LoadA load_a, const uint16_t* Bt, int M, int 
   return launch_gemm_half_tile<T>(pick_half_tile(M, N, false), load_a, Bt, M, N, K, ldb, epi, stream);
 }
 
+template <typename T, int BM, int BN, int WM, int WN, int NS, typename ASrc, typename Epi>
+static hipError_t launch_gemm_ring(ASrc asrc, const uint16_t* Bt, int M, int N, int K, int ldb, Epi epi,
+                                   hipStream_t stream) {
+  const int tiles_n = (N + BN - 1) / BN;
+  const dim3 grid(((M + BM - 1) / BM) * tiles_n);
+  hipLaunchKernelGGL((gemm_half_ring_kernel<T, BM, BN, WM, WN, NS, ASrc, Epi>), grid, dim3(WM * WN * 64), 0, stream,
+                     asrc, Bt, M, N, K, ldb, tiles_n, epi);
+  return hipGetLastError();
+}
+
+// The ring kernel serves the ViT GEMMs unless CJ_HIP_VIT_RING is 0 (A/B runs).
+inline bool vit_ring_enabled() {
+  const char* env = getenv("CJ_HIP_VIT_RING");
+  return env == nullptr || std::string(env) != "0";
+}
+
+// Its copies use 32-bit byte offsets from a stage base and 16-byte alignment.
+inline bool ring_fits(long long rows, long long ld) { return rows * ld * 2 < (1LL << 31) && ld % 8 == 0; }
+
 template <typename T, int WM, int WN>
 static hipError_t launch_gemm_lds(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda,
                                   int ldb, int ldc, hipStream_t stream) {
@@ -1238,6 +1523,14 @@ hipError_t patchEmbedGemm(const uint16_t* x, const uint16_t* Wt, uint16_t* token
   if (P % 8 != 0 || K % kHBK != 0 || W % 8 != 0) {
     return hipErrorInvalidValue;
   }
+  if (vit_ring_enabled() && (P == 8 || P == 16 || P == 32 || P == 64) &&
+      static_cast<long long>(B) * C * H * W * 2 < (1LL << 31) && ring_fits(64, K)) {
+    const RingPatch ra{x, C, H, W, P, T_, gw};
+    if (t == Half::kBF16) {
+      return launch_gemm_ring<BF16, 64, 64, 2, 2, 4>(ra, Wt, M, E, K, K, EpiHalf<BF16>{tokens, E, 1}, stream);
+    }
+    return launch_gemm_ring<F16, 64, 64, 2, 2, 4>(ra, Wt, M, E, K, K, EpiHalf<F16>{tokens, E, 1}, stream);
+  }
   const LoadPatch la{x, M, C, H, W, P, T_, gw};
   if (t == Half::kBF16) {
     return launch_gemm_half<BF16>(la, Wt, M, E, K, K, EpiHalf<BF16>{tokens, E, 1}, stream);
@@ -1251,12 +1544,39 @@ hipError_t qkvProjectGemm(const uint16_t* tokens, const uint16_t* Wqkv_t, uint16
   if (E % kHBK != 0 || E % H != 0) {
     return hipErrorInvalidValue;
   }
-  const LoadRowMajor la{tokens, E};
   const int Dh = E / H;
+  // The ring kernel's accumulator stores need whole 4-row groups per image.
+  if (vit_ring_enabled() && ring_fits(128, E) && T_ % 4 == 0) {
+    // 128x128 tiles (8 waves): 234 workgroups for the B = 8 block, one per
+    // CU; measured faster than 64x64 tiles (900 workgroups).
+    const RingRowMajor ra{tokens, E};
+    if (t == Half::kBF16) {
+      return launch_gemm_ring<BF16, 128, 128, 2, 4, 4>(ra, Wqkv_t, M, 3 * E, E, E,
+                                                       EpiQKV<BF16>{q, k, vt, T_, E, H, Dh, S_pad}, stream);
+    }
+    return launch_gemm_ring<F16, 128, 128, 2, 4, 4>(ra, Wqkv_t, M, 3 * E, E, E,
+                                                    EpiQKV<F16>{q, k, vt, T_, E, H, Dh, S_pad}, stream);
+  }
+  const LoadRowMajor la{tokens, E};
   if (t == Half::kBF16) {
     return launch_gemm_half<BF16>(la, Wqkv_t, M, 3 * E, E, E, EpiQKV<BF16>{q, k, vt, T_, E, H, Dh, S_pad}, stream);
   }
   return launch_gemm_half<F16>(la, Wqkv_t, M, 3 * E, E, E, EpiQKV<F16>{q, k, vt, T_, E, H, Dh, S_pad}, stream);
+}
+
+hipError_t outProjectGemm(const uint16_t* attn, const uint16_t* Wo_t, float* out, int M, int E, Half t,
+                          hipStream_t stream) {
+  if (E % kHBK != 0) {
+    return hipErrorInvalidValue;
+  }
+  if (vit_ring_enabled() && ring_fits(64, E)) {
+    const RingRowMajor ra{attn, E};
+    if (t == Half::kBF16) {
+      return launch_gemm_ring<BF16, 64, 64, 2, 2, 4>(ra, Wo_t, M, E, E, E, EpiF32{out, E}, stream);
+    }
+    return launch_gemm_ring<F16, 64, 64, 2, 2, 4>(ra, Wo_t, M, E, E, E, EpiF32{out, E}, stream);
+  }
+  return gemmHalfTN(attn, Wo_t, out, M, E, E, E, E, E, t, GemmHalfVariant::kAuto, stream);
 }
 
 }  // namespace lchip::kern
