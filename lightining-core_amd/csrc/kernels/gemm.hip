@@ -658,16 +658,20 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
   const uint16_t* b_tile = Bt + static_cast<size_t>(bn) * ldb;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t lds0 = lds_addr(smem);
-  auto issue = [&](int buf, int k0) {
+  // Copy q of a stage: A rows for q < LPW, then B rows.
+  auto issue_one = [&](int buf, int k0, int q) {
     const uint32_t base = lds0 + 2u * static_cast<uint32_t>(buf * STAGE);
-#pragma unroll
-    for (int j = 0; j < LPW; ++j) {
-      load_lds16_sbase(a_off[j], a_tile + k0, base + 2u * static_cast<uint32_t>((NW * j + wave_s) * 8 * BK));
+    if (q < LPW) {
+      load_lds16_sbase(a_off[q], a_tile + k0, base + 2u * static_cast<uint32_t>((NW * q + wave_s) * 8 * BK));
+    } else {
+      load_lds16_sbase(b_off[q - LPW], b_tile + k0,
+                       base + 2u * static_cast<uint32_t>(BM * BK + (NW * (q - LPW) + wave_s) * 8 * BK));
     }
+  };
+  auto issue = [&](int buf, int k0) {
 #pragma unroll
-    for (int j = 0; j < LPW; ++j) {
-      load_lds16_sbase(b_off[j], b_tile + k0,
-                       base + 2u * static_cast<uint32_t>(BM * BK + (NW * j + wave_s) * 8 * BK));
+    for (int q = 0; q < 2 * LPW; ++q) {
+      issue_one(buf, k0, q);
     }
   };
 
@@ -695,11 +699,17 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
   // Only this wave's LDS reads may be outstanding at the loop head: a pending
   // scalar load would make every LDS wait in the loop an lgkmcnt(0).
   __builtin_amdgcn_s_waitcnt(0xc07f);
+  // The next stage's copies go out one after every second MFMA of this
+  // stage's first two k-steps (8 copies per wave): issued in a burst they
+  // queue behind the other waves' copies and hold up this wave's MFMAs;
+  // spread over the whole stage the last ones land late.
+  constexpr int MPS = TM * TN;                 // MFMAs per k-step
+  constexpr int EVERY = 2;
+  constexpr int COPIES = 2 * LPW;
+  static_assert(COPIES <= 2 * MPS / EVERY, "copies fit the first two k-steps");
   for (int kt = 0; kt < nk; ++kt) {
     const int buf = kt & 1;
-    if (kt + 1 < nk) {
-      issue(buf ^ 1, (kt + 1) * BK);
-    }
+    const bool more = kt + 1 < nk;
     const uint16_t* As = smem + buf * STAGE;
     const uint16_t* Bs = As + BM * BK;
     u32x4 af[2][TM];
@@ -734,6 +744,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           acc[i][j] = mfma32x32x16<T>(af[cur][i], bf[cur][j], acc[i][j]);
+          const int mi = s * MPS + i * TN + j;  // MFMA index within the stage
+          if (mi % EVERY == EVERY - 1 && mi / EVERY < COPIES && more) {
+            __builtin_amdgcn_sched_barrier(0);
+            issue_one(buf ^ 1, (kt + 1) * BK, mi / EVERY);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
       __builtin_amdgcn_sched_barrier(0);
