@@ -428,7 +428,7 @@ PMC_GEMMS = 20
 GEMM_F32_1024_TRAFFIC = 25250119 + 4194304  # HBM bytes per launch (fetch + write, calibrated)
 
 
-def pmc_workload(lc, synth):
+def pmc_workload(lc, synth, which="c2"):
     lib = lc._core._lib()
     src, dst = ctypes.c_void_p(), ctypes.c_void_p()
     if lib.lcMalloc(ctypes.byref(src), PMC_COPY_BYTES) != 0 or lib.lcMalloc(ctypes.byref(dst), PMC_COPY_BYTES) != 0:
@@ -441,14 +441,41 @@ def pmc_workload(lc, synth):
     finally:
         lib.lcFree(src)
         lib.lcFree(dst)
-    a = synth.uniform((1024, 1024), stream=100)
-    b = synth.uniform((1024, 1024), stream=101)
-    s = lc.MatMulResidentSession(1024, 1024, 1024, "f32")
-    s.start_into(a, b)
-    s.run_batch_sync_cached_no_download(PMC_GEMMS)
+    if which == "c2":
+        a = synth.uniform((1024, 1024), stream=100)
+        b = synth.uniform((1024, 1024), stream=101)
+        s = lc.MatMulResidentSession(1024, 1024, 1024, "f32")
+        s.start_into(a, b)
+        s.run_batch_sync_cached_no_download(PMC_GEMMS)
+        lc.device_synchronize()
+        s.close()
+        log(f"[bench] pmc workload done: {PMC_COPIES} copies of {PMC_COPY_BYTES} bytes, {PMC_GEMMS} GEMM launches")
+        return
+    # "bf16": a few launches of each 16-bit config at its bench shape (the
+    # counter passes read the kernels' MFMA busy cycles and HBM bytes).
+    b_, h_, s_, d_ = 4, 16, 2048, 128
+    q, k, v = (0.5 * synth.normal((b_, h_, s_, d_), stream=210 + i) for i in range(3))
+    sess = lc.AttentionSession.batched(b_, h_, s_, d_, causal=True, compute_dtype="bf16")
+    sess.forward_with_policy(q, k, v, lc.AttentionIoPolicy(download_out=False))
+    sess.run_cached(3)
     lc.device_synchronize()
-    s.close()
-    log(f"[bench] pmc workload done: {PMC_COPIES} copies of {PMC_COPY_BYTES} bytes, {PMC_GEMMS} GEMM launches")
+    sess.close()
+    bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12
+    vs = lc.VitBlockSession(bn, c, img, img, p, e, heads, "f16")
+    vs.set_weights(synth.normal((e, c, p, p), std=0.02, stream=221), synth.normal((e, 3 * e), std=0.02, stream=222),
+                   synth.normal((e, e), std=0.02, stream=223))
+    vs.forward(synth.uniform((bn, c, img, img), lo=0.0, hi=1.0, stream=220), download=False)
+    vs.run_cached(3)
+    lc.device_synchronize()
+    vs.close()
+    for m, k_, n, reps in ((4096, 4096, 4096, 3), (8192, 8192, 8192, 2), (16, 8192, 8192, 5)):
+        sess = lc.MatMulResidentSession(m, k_, n, "bf16")
+        sess.start_into(synth.normal((m, k_), stream=230), synth.normal((k_, n), stream=231))
+        sess.run_batch_sync_cached_no_download(reps)
+        lc.device_synchronize()
+        sess.close()
+    log(f"[bench] pmc workload done: {PMC_COPIES} copies of {PMC_COPY_BYTES} bytes, then C3 x4, C4 x4, "
+        "C5 4096^3 x4, 8192^3 x3, 16x8192x8192 x6 launches (first of each from the session start)")
 
 
 def main():
@@ -457,10 +484,11 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="run only the fixed workload the rocprofv3 --pmc traffic passes count: "
-                         f"{PMC_COPIES} device-to-device copies of {PMC_COPY_BYTES >> 20} MiB (calibration) "
-                         f"and {PMC_GEMMS} launches of the 1024^3 fp32 GEMM")
+    ap.add_argument("--pmc-workload", nargs="?", const="c2", default=None, choices=("c2", "bf16"),
+                    help="run only the fixed workload the rocprofv3 --pmc passes count: "
+                         f"{PMC_COPIES} device-to-device copies of {PMC_COPY_BYTES >> 20} MiB (calibration), "
+                         f"then {PMC_GEMMS} launches of the 1024^3 fp32 GEMM (c2, the default) or a few launches "
+                         "of each 16-bit config (bf16)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py: this build measures one GPU only (the path is single-GPU; see DESIGN.md for how it would "
@@ -476,7 +504,7 @@ def main():
     info = lc.device_info()
     log(f"[bench] device {info}")
     if args.pmc_workload:
-        pmc_workload(lc, synth)
+        pmc_workload(lc, synth, args.pmc_workload)
         return
     cpu = CpuBaseline()
     value, ms_per_step, roofline, cpu_obj = bench_config2(lc, synth, args.steps, args.warmup, cpu)
