@@ -155,6 +155,35 @@ def test_vit_block_small(lc, oracle, dtype):
     assert_parity(ref, got.reshape(ref.shape), dtype, f"vit small {dtype}")
 
 
+# Shapes for the ring-pipelined ViT GEMMs: P = 8 and 32 patch sources, token
+# counts that are not tile multiples (rows clamped), and T % 4 != 0, which
+# sends the QKV projection to the element-wise epilogue.
+@pytest.mark.parametrize("bn,img,p,e,heads,dtype", [
+    (3, 40, 8, 128, 2, "f16"),     # T = 25 (T % 4 != 0), M = 75
+    (5, 96, 16, 192, 3, "bf16"),   # T = 36, M = 180, three heads of 64
+    (2, 64, 32, 128, 1, "f16"),    # P = 32, T = 4, one head of 128
+    (1, 48, 16, 128, 2, "bf16"),   # M = 9, a single partial tile
+])
+def test_vit_block_shapes(lc, oracle, bn, img, p, e, heads, dtype):
+    note(f"[case] vit bn={bn} img={img} p={p} e={e} heads={heads} {dtype}")
+    x, w_conv, w_qkv, w_o = _vit_inputs(bn, 3, img, p, e)
+    got = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype=dtype)
+    ref = oracle.vit_block(*(synth.round_to(t, dtype) for t in (x, w_conv, w_qkv, w_o)), heads)
+    assert_parity(ref, got.reshape(ref.shape), dtype, f"vit {bn}x{img} p{p} e{e} {dtype}")
+
+
+def test_vit_block_ring_off_matches(lc, monkeypatch):
+    # CJ_HIP_VIT_RING=0 keeps the register-staged GEMMs: same inputs, results
+    # within the 16-bit tolerance of the ring path (the k order of the
+    # accumulation is the same; only the tiling differs).
+    bn, c, img, p, e, heads = 2, 3, 64, 16, 128, 2
+    x, w_conv, w_qkv, w_o = _vit_inputs(bn, c, img, p, e)
+    ring = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype="f16")
+    monkeypatch.setenv("CJ_HIP_VIT_RING", "0")
+    plain = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype="f16")
+    assert np.abs(ring - plain).max() <= 2e-2 * np.abs(plain).max()
+
+
 def test_vit_block_config4(lc, oracle):
     bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12
     note("[case] config 4 ViT block")
