@@ -570,15 +570,49 @@ __global__ __launch_bounds__(64 * KS) void attn_dv_f32_kernel(const float* __res
   const int key = j0 + (lane & 31);
   const int nqt = (S + 31) / 32;
   // Causal: query tile I meets key block J only when some query >= some key.
+  const bool vec = (D & 3) == 0;
   for (int qt = (causal ? blockIdx.x : 0) + wave; qt < nqt; qt += KS) {
     const int i0 = qt * 32;
-    for (int idx = lane; idx < 32 * DP; idx += 64) {
-      const int r = idx / DP;
-      const int cc = idx - r * DP;
-      const bool ok = i0 + r < S && cc < D;
-      const size_t off = static_cast<size_t>(i0 + r) * D + cc;
-      Qs[r][cc] = ok ? q[off] : 0.0f;
-      Gs[r][cc] = ok ? 2.0f * (out[off] - target[off]) * norm : 0.0f;
+    // This lane's 16 queries' softmax statistics, loaded first so their
+    // latency overlaps the tile fills and QK^T.
+    float sm[16];
+    float sl[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = min(i0 + acc_row(r, lane), S - 1);
+      sm[r] = stats[static_cast<size_t>(qi) * 2];
+      sl[r] = stats[static_cast<size_t>(qi) * 2 + 1];
+    }
+    if (vec) {
+      // float4 fills (D % 4 == 0: a chunk is all inside or all past D).
+      for (int idx = lane; idx < 32 * (DP / 4); idx += 64) {
+        const int r = idx / (DP / 4);
+        const int cc = (idx - r * (DP / 4)) * 4;
+        float4 qv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 gv = qv;
+        if (i0 + r < S && cc < D) {
+          const size_t off = static_cast<size_t>(i0 + r) * D + cc;
+          qv = *reinterpret_cast<const float4*>(q + off);
+          const float4 ov = *reinterpret_cast<const float4*>(out + off);
+          const float4 tv = *reinterpret_cast<const float4*>(target + off);
+          const float g = 2.0f * norm;
+          gv = make_float4((ov.x - tv.x) * g, (ov.y - tv.y) * g, (ov.z - tv.z) * g, (ov.w - tv.w) * g);
+        }
+        Qs[r][cc] = qv.x;
+        Qs[r][cc + 1] = qv.y;
+        Qs[r][cc + 2] = qv.z;
+        Qs[r][cc + 3] = qv.w;
+        *reinterpret_cast<float4*>(&Gs[r][cc]) = gv;
+      }
+    } else {
+      for (int idx = lane; idx < 32 * DP; idx += 64) {
+        const int r = idx / DP;
+        const int cc = idx - r * DP;
+        const bool ok = i0 + r < S && cc < D;
+        const size_t off = static_cast<size_t>(i0 + r) * D + cc;
+        Qs[r][cc] = ok ? q[off] : 0.0f;
+        Gs[r][cc] = ok ? 2.0f * (out[off] - target[off]) * norm : 0.0f;
+      }
     }
     __builtin_amdgcn_wave_barrier();
     // S = Q . K^T: A = Q rows (query), B = K^T (lane: key, k = d).
@@ -594,9 +628,7 @@ __global__ __launch_bounds__(64 * KS) void attn_dv_f32_kernel(const float* __res
       const int qi = i0 + acc_row(r, lane);
       float p = 0.0f;
       if (qi < S && key < S && !(causal && key > qi)) {
-        const float m = stats[static_cast<size_t>(qi) * 2];
-        const float l = stats[static_cast<size_t>(qi) * 2 + 1];
-        p = exp2f((st[r] * scale) * kLog2e - m) / l;
+        p = exp2f((st[r] * scale) * kLog2e - sm[r]) / sl[r];
       }
       st[r] = p;
     }
