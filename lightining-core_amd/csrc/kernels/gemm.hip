@@ -1111,21 +1111,32 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
   int is_k = (it1 - 1) - is_t * nk;
   int is_bm, is_bn;
   origin(is_t, is_bm, is_bn);
-  auto issue_next = [&](int buf) {
+  // Copy q of the cursor's stage into buffer buf: A for q < LPW, then B.
+  auto issue_copy = [&](int buf, int q) {
     const uint32_t base = lds0 + 4u * static_cast<uint32_t>(buf * STAGE);
-    const float* a_base = A + static_cast<size_t>(is_bm) * lda + is_k * BK;
-    const float* b_base = B + static_cast<size_t>(is_k) * BK * ldb + is_bn;
-#pragma unroll
-    for (int j = 0; j < LPW; ++j) {
-      load_lds16_sbase(a_off[j], a_base, base + 4u * static_cast<uint32_t>((wave_s + NW * j) * 256));
-      load_lds16_sbase(b_off[j], b_base, base + 4u * static_cast<uint32_t>(A_STAGE + (wave_s + NW * j) * 256));
+    if (q < LPW) {
+      const float* a_base = A + static_cast<size_t>(is_bm) * lda + is_k * BK;
+      load_lds16_sbase(a_off[q], a_base, base + 4u * static_cast<uint32_t>((wave_s + NW * q) * 256));
+    } else {
+      const float* b_base = B + static_cast<size_t>(is_k) * BK * ldb + is_bn;
+      load_lds16_sbase(b_off[q - LPW], b_base,
+                       base + 4u * static_cast<uint32_t>(A_STAGE + (wave_s + NW * (q - LPW)) * 256));
     }
+  };
+  auto advance = [&]() {
     if (--is_k < 0) {
       is_k = nk - 1;
       if (--is_t >= 0) {
         origin(is_t, is_bm, is_bn);
       }
     }
+  };
+  auto issue_next = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < 2 * LPW; ++q) {
+      issue_copy(buf, q);
+    }
+    advance();
   };
 
   floatx16 acc0 = zero16();
@@ -1249,9 +1260,11 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
       wait_vmcnt<0>();
     }
     stage_barrier();
-    if (j + STAGES - 1 < n_it) {
-      issue_next((j + STAGES - 1) % STAGES);
-    }
+    // The next stage's copies go out one after every second MFMA of this
+    // stage's first half (a burst behind the barrier queues every wave's
+    // copies at once); the cursor advances after the last one.
+    const bool more = j + STAGES - 1 < n_it;
+    const int nbuf = (j + STAGES - 1) % STAGES;
     const float* As = smem + (j % STAGES) * STAGE;
     const float* Bs = As + A_STAGE;
     floatx4 a[GPW];
@@ -1272,10 +1285,23 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int g = 0; g < GPW; ++g) {
-      acc0 = mfma32x32x2f32(a[g][0], b[g][0], acc0);
-      acc1 = mfma32x32x2f32(a[g][1], b[g][1], acc1);
-      acc0 = mfma32x32x2f32(a[g][2], b[g][2], acc0);
-      acc1 = mfma32x32x2f32(a[g][3], b[g][3], acc1);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (u % 2 == 0) {
+          acc0 = mfma32x32x2f32(a[g][u], b[g][u], acc0);
+        } else {
+          acc1 = mfma32x32x2f32(a[g][u], b[g][u], acc1);
+        }
+        const int mi = 4 * g + u;
+        if (mi % 2 == 1 && mi / 2 < 2 * LPW && more) {
+          __builtin_amdgcn_sched_barrier(0);
+          issue_copy(nbuf, mi / 2);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    if (more) {
+      advance();
     }
     if constexpr (SK) {
       if (ck == 0 || j == n_it - 1) {
