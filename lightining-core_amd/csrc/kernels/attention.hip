@@ -748,9 +748,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   constexpr int QS = D / 16;
   static_assert(D == 64 || D == 128, "head dim");
   // One LDS array: K buffers at 0 and TILE, V^T buffers at 2*TILE and
-  // 3*TILE.  (With separate __shared__ arrays the compiler puts a full
-  // vmcnt(0) in front of the first LDS read after every global -> LDS load,
-  // which would expose the load latency of each tile.)
+  // 3*TILE (copies address it by byte offset from its base).
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * TILE];
 
   const int tid = threadIdx.x;

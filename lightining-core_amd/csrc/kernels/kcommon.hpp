@@ -113,18 +113,6 @@ __device__ __forceinline__ floatx16 zero16() {
   return z;
 }
 
-// 16-byte global -> LDS copy of one lane (LDS address = lds_base + 16*lane).
-// A plain (non-template) device function: used directly inside a kernel
-// template whose body depends on template parameters, the target builtin
-// makes the host-side instantiation fail silently and no launch stub is
-// emitted.
-__device__ __forceinline__ void load_lds16(const uint16_t* src, uint16_t* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
-}
-__device__ __forceinline__ void load_lds16(const float* src, float* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, lds_base, 16, 0, 0);
-}
-
 // 16-byte global -> LDS copy of one lane from a wave-uniform base and a
 // 32-bit per-lane byte offset (LDS address = lds + 16*lane), written as
 // inline asm for two reasons:
