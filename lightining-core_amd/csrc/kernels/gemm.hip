@@ -775,6 +775,174 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_lds_kernel(const uin
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit TN GEMM for grids of at least two 256x256 tiles per CU: 4 waves of
+// 128x128 (one per SIMD, accumulators in the AGPRs), against the 8 waves of
+// 128x64 above: half the LDS fragment reads per MFMA.
+//
+// LDS holds a ring of four 32-deep k slices (32 KB each: 256 A rows then 256
+// B rows of 64 bytes, 16-byte chunk c of row r at physical chunk
+// c ^ ((r >> 2) & 3), conflict-free for the fragment reads).  During slice h
+// a wave issues its 8 copies of slice h + 3 (into the slot slice h - 1 left,
+// one after every fourth MFMA), reads the fragments of k-step 1 of slice h
+// and then k-step 0 of slice h + 1 while its MFMAs run; at the end of slice h
+// it waits for its copies of slice h + 2 and the barrier publishes them, so
+// no fragment read waits on a barrier.  Past the last slice the copies
+// re-load slice H - 1 into slots already retired and the reads of slot
+// (h + 1) & 3 return unused data: every iteration has the same waits.
+//
+// The k order of each accumulator matches gemm_half_tn_lds_kernel, so the two
+// give bit-identical results.  Tiles are ordered in groups of 4 tile rows per
+// XCD (measured on 8192^3: 4 > 8 > 16 by 1% and 13%).  Operands are padded to
+// 256 rows and copies use 32-bit lane offsets: the host keeps 256 * ld * 2
+// bytes below 2^31.
+// ---------------------------------------------------------------------------
+template <typename T, typename Epi>
+__global__ __launch_bounds__(256) void gemm_half_tn_w4_kernel(const uint16_t* __restrict__ A,
+                                                              const uint16_t* __restrict__ Bt, int M, int N, int K,
+                                                              int lda, int ldb, int tiles_n, Epi epi) {
+  constexpr int BM = 256, BN = 256, HK = 32;
+  constexpr int ROWB = HK * 2;            // bytes per LDS row (64)
+  constexpr int SLOT = (BM + BN) * HK;    // elements per slot
+  __shared__ __attribute__((aligned(16))) uint16_t smem[4 * SLOT];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+
+  constexpr int GROUP = 4;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int nwg = gridDim.x;
+  const int full = nwg & ~7;
+  int pid = blockIdx.x;
+  if (pid < full) {
+    pid = (pid & 7) * (full >> 3) + (pid >> 3);
+  }
+  const int group_size = GROUP * tiles_n;
+  const int group = pid / group_size;
+  const int first_m = group * GROUP;
+  const int gm = min(tiles_m - first_m, GROUP);
+  const int in_group = pid - group * group_size;
+  const int bm = (first_m + in_group % gm) * BM;
+  const int bn = (in_group / gm) * BN;
+
+  // Copy instruction i (0..15 per operand per slice) fills rows 16i + lane/4,
+  // physical chunk lane%4; wave w issues i = w + 4j, j = 0..3.
+  const int crow = lane >> 2;
+  const int pch = lane & 3;
+  uint32_t a_off[4];
+  uint32_t b_off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 16 * (wave + 4 * j) + crow;
+    const int lch = pch ^ ((row >> 2) & 3);
+    a_off[j] = static_cast<uint32_t>(row * lda + lch * 8) * 2u;
+    b_off[j] = static_cast<uint32_t>(row * ldb + lch * 8) * 2u;
+  }
+  const uint16_t* a_tile = A + static_cast<size_t>(bm) * lda;
+  const uint16_t* b_tile = Bt + static_cast<size_t>(bn) * ldb;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = lds_addr(smem);
+  // Copy q (0..7) of slice h into ring slot `slot`: A rows for q < 4, then B.
+  auto issue_one = [&](int h, int q, int slot) {
+    const uint32_t base = lds0 + 2u * static_cast<uint32_t>((slot & 3) * SLOT);
+    const int k0 = h * HK;
+    if (q < 4) {
+      load_lds16_sbase(a_off[q], a_tile + k0, base + static_cast<uint32_t>((wave_s + 4 * q) * 1024));
+    } else {
+      load_lds16_sbase(b_off[q - 4], b_tile + k0,
+                       base + 2u * BM * HK + static_cast<uint32_t>((wave_s + 4 * (q - 4)) * 1024));
+    }
+  };
+
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  // Fragment f (0..7) of k-step s of slice h: A rows for f < 4, then B rows.
+  auto frag = [&](int h, int s, int f) -> u32x4 {
+    const char* base = reinterpret_cast<const char*>(smem + (h & 3) * SLOT);
+    const int row = f < 4 ? wm + f * 32 + lrow : wn + (f - 4) * 32 + lrow;
+    const int opoff = f < 4 ? 0 : 2 * BM * HK;
+    const int c = 2 * s + lhalf;
+    return *reinterpret_cast<const u32x4*>(base + opoff + row * ROWB + ((c ^ ((row >> 2) & 3)) << 4));
+  };
+
+  floatx16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[i][j] = zero16();
+    }
+  }
+
+  const int H = K / HK;
+#pragma unroll
+  for (int h = 0; h < 3; ++h) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      issue_one(min(h, H - 1), q, h);
+    }
+  }
+  wait_vmcnt<8>();                     // slices 0 and 1 have landed
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // no scalar load pending at the loop head
+  stage_barrier();
+  u32x4 f0[8];
+  u32x4 f1[8];
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    f0[f] = frag(0, 0, f);
+  }
+  for (int h = 0; h < H; ++h) {
+    const int hc = min(h + 3, H - 1);
+    // k-step 0: MFMAs on f0; f1 <- k-step 1 of slice h; copies 0..3
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = mfma32x32x16<T>(f0[i >> 2], f0[4 + (i & 3)], acc[i >> 2][i & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        f1[i] = frag(h, 1, i);
+      }
+      if ((i & 3) == 3) {
+        issue_one(hc, i >> 2, h + 3);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // k-step 1: MFMAs on f1; f0 <- k-step 0 of slice h + 1; copies 4..7
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = mfma32x32x16<T>(f1[i >> 2], f1[4 + (i & 3)], acc[i >> 2][i & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        f0[i] = frag(h + 1, 0, i);
+      }
+      if ((i & 3) == 3) {
+        issue_one(hc, 4 + (i >> 2), h + 3);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vmcnt<8>();  // this wave's copies of slice h + 2 have landed
+    stage_barrier();  // everyone's have: slice h + 2 is readable, slot (h & 3) is free
+  }
+  wait_vmcnt<0>();    // no copy may still be writing LDS when the wave ends
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = bn + wn + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = bm + wm + i * 32 + acc_row(r, lane);
+        if (m < M && n < N) {
+          epi(m, n, acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Ring-pipelined 16-bit TN GEMM for short K (the ViT block's GEMMs, K = 768).
 //
 // With K = 768 a tile has 12 stages of BK = 64 and each stage holds only a
@@ -1322,6 +1490,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 }
 
 // Tile configurations (block tile BM x BN, waves WM x WN, BK = 64):
+//   w4     256x256, 4 waves 2x2 (128x128 each), ring of 32-deep slices
+//          (gemm_half_tn_w4_kernel); needs A / Bt padded to 256 rows
 //   lds    256x256, 8 waves 2x4 (128x64 each), global -> LDS direct loads
 //          (gemm_half_tn_lds_kernel); needs A / Bt padded to 256 rows
 //   big8   256x256, 8 waves 2x4, LDS double buffer fed from registers
@@ -1329,16 +1499,19 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 //   mid    128x128, 4 waves 2x2 (64x64 each)
 //   small   64x64,  4 waves 2x2 (32x32 each)
 // Default: the largest tile that still gives at least one workgroup per CU
-// (lds where the operands are padded, big8 elsewhere).
+// (w4 from two tiles per CU and lds below that where the operands are padded,
+// big8 elsewhere; measured 8192^3 bf16: w4 1300-1310 against lds 1230-1265
+// TFLOP/s, 4096^3: lds 1245-1260 against w4 1220-1230).
 // CJ_HIP_GEMM_TILE=<name> overrides the choice (tuning sweeps), like the
 // reference's CJ_* tuning variables.
-enum class HalfTile { kLds, kBig8, kBig4, kMid, kSmall };
+enum class HalfTile { kW4, kLds, kBig8, kBig4, kMid, kSmall };
 
 inline int tiles_for(int M, int N, int b) { return ((M + b - 1) / b) * ((N + b - 1) / b); }
 
 inline HalfTile pick_half_tile(int M, int N, bool padded) {
   if (const char* env = getenv("CJ_HIP_GEMM_TILE")) {
     const std::string v(env);
+    if (v == "w4" && padded) return HalfTile::kW4;
     if (v == "lds" && padded) return HalfTile::kLds;
     if (v == "big8") return HalfTile::kBig8;
     if (v == "big4") return HalfTile::kBig4;
@@ -1346,6 +1519,9 @@ inline HalfTile pick_half_tile(int M, int N, bool padded) {
     if (v == "small") return HalfTile::kSmall;
   }
   constexpr int kCUs = 256;
+  if (tiles_for(M, N, 256) >= 2 * kCUs) {
+    return padded ? HalfTile::kW4 : HalfTile::kBig8;
+  }
   if (tiles_for(M, N, 256) >= kCUs) {
     return padded ? HalfTile::kLds : HalfTile::kBig8;
   }
@@ -1369,6 +1545,7 @@ template <typename T, typename LoadA, typename Epi>
 static hipError_t launch_gemm_half_tile(HalfTile tile, LoadA load_a, const uint16_t* Bt, int M, int N, int K,
                                         int ldb, Epi epi, hipStream_t stream) {
   switch (tile) {
+    case HalfTile::kW4:
     case HalfTile::kLds:
     case HalfTile::kBig8:
       return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
@@ -1406,6 +1583,16 @@ inline bool vit_ring_enabled() {
 
 // Its copies use 32-bit byte offsets from a stage base and 16-byte alignment.
 inline bool ring_fits(long long rows, long long ld) { return rows * ld * 2 < (1LL << 31) && ld % 8 == 0; }
+
+template <typename T>
+static hipError_t launch_gemm_w4(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda,
+                                 int ldb, int ldc, hipStream_t stream) {
+  const int tiles_n = (N + 255) / 256;
+  const dim3 grid(((M + 255) / 256) * tiles_n);
+  hipLaunchKernelGGL((gemm_half_tn_w4_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
+                     tiles_n, EpiF32{C, ldc});
+  return hipGetLastError();
+}
 
 template <typename T, int WM, int WN>
 static hipError_t launch_gemm_lds(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda,
@@ -1489,6 +1676,7 @@ GemmHalfVariant gemmHalfChoose(int M, int N) {
     return GemmHalfVariant::kSkinny;
   }
   switch (pick_half_tile(M, N, true)) {
+    case HalfTile::kW4: return GemmHalfVariant::kW4;
     case HalfTile::kLds: return GemmHalfVariant::kLds;
     case HalfTile::kBig8: return GemmHalfVariant::kBig8;
     case HalfTile::kBig4: return GemmHalfVariant::kBig4;
@@ -1510,9 +1698,13 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
   }
   // A and Bt come from the resident upload, padded to 256 rows; the copies'
   // 32-bit lane offsets reach 256 rows of either operand.
-  if (variant == GemmHalfVariant::kLds &&
+  if ((variant == GemmHalfVariant::kLds || variant == GemmHalfVariant::kW4) &&
       (256LL * lda * 2 >= (1LL << 31) || 256LL * ldb * 2 >= (1LL << 31))) {
     variant = GemmHalfVariant::kBig8;
+  }
+  if (variant == GemmHalfVariant::kW4 && K > 0) {
+    return t == Half::kBF16 ? launch_gemm_w4<BF16>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
+                            : launch_gemm_w4<F16>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
   }
   if (variant == GemmHalfVariant::kLds && K > 0) {
     return t == Half::kBF16 ? launch_gemm_lds<BF16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
