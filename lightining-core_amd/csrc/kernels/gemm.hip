@@ -1189,7 +1189,9 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, 
 // partial tile (part[w], flag[w] = 1) as soon as it is done; the segment
 // holding the last stage owns the tile: it waits for the flags of the lower
 // workgroups that hold the rest, adds their partials in workgroup order
-// (deterministic) and stores.  Waits only ever target lower workgroup ids,
+// (deterministic) and stores.  With xl set, each XCD's workgroups split only
+// the iterations of that XCD's own contiguous range of tiles (the same
+// protocol among the ranks of one XCD).  Waits only ever target lower workgroup ids,
 // which the in-order dispatch has already started, and each spin is bounded,
 // so every wave exits.  With T a multiple of G (1024^3: 256 tiles on 256
 // CUs) every range is whole tiles and nothing is published.  The owner
@@ -1204,7 +1206,7 @@ template <int BK, int STAGES, int KS, bool SK, typename Epi>
 __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                            int M, int N, int lda, int ldb, int tiles_m, int tiles_n,
                                                            int nk, float* __restrict__ part, int* __restrict__ flags,
-                                                           Epi epi) {
+                                                           Epi epi, int xl = 0) {
   constexpr int BM = 64, BN = 64;
   constexpr int A_STAGE = BM * BK;            // floats
   constexpr int STAGE = (BM + BN) * BK;       // floats
@@ -1229,11 +1231,21 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
   const int G = gridDim.x;
   const int w = blockIdx.x;
   const int T = tiles_m * tiles_n;
-  const long long I = static_cast<long long>(T) * nk;
-  auto begin_of = [&](int q) { return static_cast<int>(static_cast<long long>(q) * I / G); };
+  // XCD-local stream-K (xl, G % 8 == 0, T >= 8): workgroup w runs on XCD
+  // w % 8; the G / 8 workgroups of an XCD (rank w / 8) split the iterations
+  // of that XCD's own contiguous range of tiles, so operand tiles, partials
+  // and flags stay in one L2.  Otherwise one range over all tiles.
+  const int xcd = xl ? (w & 7) : 0;
+  const int rank = xl ? (w >> 3) : w;
+  const int Gs = xl ? (G >> 3) : G;
+  const int tile0 = xl ? xcd * T / 8 : 0;
+  const int Ts = xl ? (xcd + 1) * T / 8 - tile0 : T;
+  const long long I = static_cast<long long>(Ts) * nk;
+  auto begin_of = [&](int q) { return static_cast<int>(static_cast<long long>(q) * I / Gs); };
+  auto wg_of = [&](int q) { return xl ? q * 8 + xcd : q; };
   // !SK: one whole tile per workgroup (G == T), no partials.
-  const int it0 = SK ? begin_of(w) : w * nk;
-  const int it1 = SK ? begin_of(w + 1) : it0 + nk;
+  const int it0 = SK ? begin_of(rank) : w * nk;
+  const int it1 = SK ? begin_of(rank + 1) : it0 + nk;
   const int n_it = it1 - it0;
   if (n_it <= 0) {
     return;
@@ -1244,8 +1256,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
   // gives each XCD a contiguous pid range, walked in groups of 8 tile rows.
   auto origin = [&](int t, int& bm, int& bn) {
     const int full = T & ~7;
-    int pid = t;
-    if (pid < full) {
+    int pid = tile0 + t;
+    if (!xl && pid < full) {
       pid = (pid & 7) * (full >> 3) + (pid >> 3);
     }
     const int group_size = 8 * tiles_n;
@@ -1359,20 +1371,20 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
       return;
     }
     if (!has_first) {
-      int wf = static_cast<int>(static_cast<long long>(t) * nk * G / I);
-      while (wf + 1 < G && begin_of(wf + 1) <= t * nk) {
+      int wf = static_cast<int>(static_cast<long long>(t) * nk * Gs / I);
+      while (wf + 1 < Gs && begin_of(wf + 1) <= t * nk) {
         ++wf;
       }
       while (wf > 0 && begin_of(wf) > t * nk) {
         --wf;
       }
       if (tid == 0) {
-        for (int q = wf; q < w; ++q) {
+        for (int q = wf; q < rank; ++q) {
           if (begin_of(q) == begin_of(q + 1)) {
             continue;
           }
           for (int spin = 0; spin < (1 << 22); ++spin) {
-            if (__hip_atomic_load(flags + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
+            if (__hip_atomic_load(flags + wg_of(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
               break;
             }
             __builtin_amdgcn_s_sleep(4);
@@ -1381,8 +1393,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
       }
       stage_barrier();
       if (kh == 0) {
-        for (int q = wf; q < w; ++q) {
-          float* theirs = part + static_cast<size_t>(q) * 4096 + sub * 1024 + lane;
+        for (int q = wf; q < rank; ++q) {
+          float* theirs = part + static_cast<size_t>(wg_of(q)) * 4096 + sub * 1024 + lane;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             v[i] += __hip_atomic_load(theirs + i * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1390,8 +1402,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
         }
       }
       if (tid == 0) {
-        for (int q = wf; q < w; ++q) {
-          __hip_atomic_store(flags + q, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int q = wf; q < rank; ++q) {
+          __hip_atomic_store(flags + wg_of(q), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
@@ -1652,16 +1664,20 @@ hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N,
   const EpiStoreF32 epi{C, ldc};
   if (bk32) {
     hipLaunchKernelGGL((gemm_f32_lds_kernel<32, 4, 2, false, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A,
-                       B, M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
+                       B, M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi, 0);
   } else if (sk) {
     // Two stages (80 KB of LDS): measured fastest on every shape tried
     // (1024^3 to 4096x4096x1024, stream-K and whole tiles): a shorter
     // prologue, and room for two workgroups per CU on large grids.
+    // XCD-local ranges below two tiles per workgroup (measured: 1000x777x1030
+    // 24.9 -> 23.8 us; with more tiles per workgroup an XCD's concurrent tiles
+    // scatter over its range: 1500^3 71.6 -> 77.4 us, so the global order stays).
+    const int xl = (groups % 8 == 0 && tiles >= 8 && tiles < 2 * groups) ? 1 : 0;
     hipLaunchKernelGGL((gemm_f32_lds_kernel<64, 2, 2, true, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A, B,
-                       M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
+                       M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi, xl);
   } else {
     hipLaunchKernelGGL((gemm_f32_lds_kernel<64, 2, 2, false, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A, B,
-                       M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi);
+                       M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi, 0);
   }
   return hipGetLastError();
 }

@@ -48,11 +48,15 @@ def test_matmul_f32_config2(lc, oracle, m, k, n):
     assert_parity(oracle.matmul(a, b), got, "f32", f"f32 {m}x{k}x{n}")
 
 
-@pytest.mark.parametrize("m,k,n", [(64, 8192, 64), (512, 4096, 512), (130, 1000, 70), (2048, 96, 2100), (65, 4500, 1)])
+@pytest.mark.parametrize("m,k,n", [(64, 8192, 64), (512, 4096, 512), (130, 1000, 70), (2048, 96, 2100), (65, 4500, 1),
+                                   (700, 640, 900), (1000, 777, 1030)])
 def test_matmul_f32_split_tiles(lc, oracle, m, k, n):
     # Shapes whose stream-K split puts one tile on several workgroups (up to
     # 128 partial tiles for 64x8192x64): the sum must match and be the same
-    # bits on every run (partials are added in a fixed order).
+    # bits on every run (partials are added in a fixed order).  512x4096x512,
+    # 700x640x900 (165 tiles: XCD ranges of 20 and 21) and 1000x777x1030 take
+    # the XCD-local split (fewer than two tiles per workgroup); 2048x96x2100
+    # the global one.
     a = synth.uniform((m, k), stream=13)
     b = synth.uniform((k, n), stream=14)
     s = lc.MatMulResidentSession(m, k, n, "f32")
