@@ -104,11 +104,14 @@ hipError_t convertTransposePad(const float* src, uint16_t* dst, int batch, int r
 // C[M,N] (fp32, ldc) = A[M,K] . Bt[N,K]^T with A, Bt 16-bit row-major (lda,
 // ldb), K a multiple of kHalfGemmBK, A readable up to roundup(M, 256) rows and
 // Bt up to roundup(N, 256) rows.  Variants (block tile, waves): kW4 256x256
-// with 4 waves and a ring of 32-deep k slices, kLds 256x256 with 8 waves, both
-// with direct global->LDS loads; kBig8 / kBig4 256x256 with 8 / 4 waves, kMid
-// 128x128, kSmall 64x64, kSkinny for M <= 16; kAuto follows gemmHalfChoose
-// (CJ_HIP_GEMM_TILE=w4|lds|big8|big4|mid|small overrides it).
-enum class GemmHalfVariant { kAuto = 0, kLds = 1, kBig8 = 2, kBig4 = 3, kMid = 4, kSmall = 5, kSkinny = 6, kW4 = 7 };
+// with 4 waves and a ring of 32-deep k slices, kW4D the same waves over two
+// 64-deep stages, kLds 256x256 with 8 waves, all three with direct
+// global->LDS loads; kBig8 / kBig4 256x256 with 8 / 4 waves, kMid 128x128,
+// kSmall 64x64, kSkinny for M <= 16; kAuto follows gemmHalfChoose
+// (CJ_HIP_GEMM_TILE=w4|w4d|lds|big8|big4|mid|small overrides it).
+enum class GemmHalfVariant {
+  kAuto = 0, kLds = 1, kBig8 = 2, kBig4 = 3, kMid = 4, kSmall = 5, kSkinny = 6, kW4 = 7, kW4D = 8
+};
 GemmHalfVariant gemmHalfChoose(int M, int N);
 hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda, int ldb,
                       int ldc, Half t, GemmHalfVariant variant, hipStream_t stream);

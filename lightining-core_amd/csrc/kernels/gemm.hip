@@ -943,6 +943,158 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4_kernel(const uint16_t* __
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit TN GEMM for grids of one to two 256x256 tiles per CU: the 4 waves of
+// 128x128 of gemm_half_tn_w4_kernel over two 64-deep LDS stages with
+// 128-byte rows (the swizzle of gemm_half_tn_lds_kernel), so each copy moves
+// whole 128-byte lines.  Two barriers per stage: B1 at a stage's start
+// (everyone is done with the other buffer, which the next stage's copies
+// refill: 16 per wave, one after every second MFMA of k-steps 0 and 1) and
+// B2 after k-step 2 (the wave has waited for its copies; the barrier makes
+// the next stage readable), so k-step 3 already reads the next stage's first
+// fragments.  Past the last stage the copies re-load it into the free buffer
+// (unused).  Same k order per accumulator as the other two kernels
+// (bit-identical results).  Measured on 4096^3 bf16: 1267-1289 TFLOP/s
+// against 1240-1260 for gemm_half_tn_lds_kernel; on 8192^3 it trails
+// gemm_half_tn_w4_kernel (1259-1284 against 1297-1310).
+// ---------------------------------------------------------------------------
+template <typename T, typename Epi>
+__global__ __launch_bounds__(256) void gemm_half_tn_w4d_kernel(const uint16_t* __restrict__ A,
+                                                               const uint16_t* __restrict__ Bt, int M, int N, int K,
+                                                               int lda, int ldb, int tiles_n, Epi epi) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int ROWB = BK * 2;            // bytes per LDS row (128)
+  constexpr int STAGE = (BM + BN) * BK;   // elements per stage
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+
+  constexpr int GROUP = 8;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int nwg = gridDim.x;
+  const int full = nwg & ~7;
+  int pid = blockIdx.x;
+  if (pid < full) {
+    pid = (pid & 7) * (full >> 3) + (pid >> 3);
+  }
+  const int group_size = GROUP * tiles_n;
+  const int group = pid / group_size;
+  const int first_m = group * GROUP;
+  const int gm = min(tiles_m - first_m, GROUP);
+  const int in_group = pid - group * group_size;
+  const int bm = (first_m + in_group % gm) * BM;
+  const int bn = (in_group / gm) * BN;
+
+  // Copy instruction i (0..31 per operand per stage) fills rows 8i + lane/8,
+  // physical chunk lane%8; wave w issues i = w + 4j, j = 0..7.
+  const int crow = lane >> 3;
+  const int pch = lane & 7;
+  uint32_t a_off[8];
+  uint32_t b_off[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int row = 8 * (wave + 4 * j) + crow;
+    const int lch = pch ^ ((row >> 1) & 7);
+    a_off[j] = static_cast<uint32_t>(row * lda + lch * 8) * 2u;
+    b_off[j] = static_cast<uint32_t>(row * ldb + lch * 8) * 2u;
+  }
+  const uint16_t* a_tile = A + static_cast<size_t>(bm) * lda;
+  const uint16_t* b_tile = Bt + static_cast<size_t>(bn) * ldb;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = lds_addr(smem);
+  // Copy q (0..15) of stage kt into buffer buf: A rows for q < 8, then B.
+  auto issue_one = [&](int kt, int q, int buf) {
+    const uint32_t base = lds0 + 2u * static_cast<uint32_t>((buf & 1) * STAGE);
+    const int k0 = kt * BK;
+    if (q < 8) {
+      load_lds16_sbase(a_off[q], a_tile + k0, base + static_cast<uint32_t>((wave_s + 4 * q) * 1024));
+    } else {
+      load_lds16_sbase(b_off[q - 8], b_tile + k0,
+                       base + 2u * BM * BK + static_cast<uint32_t>((wave_s + 4 * (q - 8)) * 1024));
+    }
+  };
+
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  // Fragment f (0..7) of k-step s of the stage in buffer buf: A rows for
+  // f < 4, then B rows.
+  auto frag = [&](int buf, int s, int f) -> u32x4 {
+    const char* base = reinterpret_cast<const char*>(smem + (buf & 1) * STAGE);
+    const int row = f < 4 ? wm + f * 32 + lrow : wn + (f - 4) * 32 + lrow;
+    const int opoff = f < 4 ? 0 : 2 * BM * BK;
+    const int c = 2 * s + lhalf;
+    return *reinterpret_cast<const u32x4*>(base + opoff + row * ROWB + ((c ^ ((row >> 1) & 7)) << 4));
+  };
+
+  floatx16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[i][j] = zero16();
+    }
+  }
+
+  const int nk = K / BK;
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    issue_one(0, q, 0);
+  }
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // no scalar load pending at the loop head
+  stage_barrier();
+  u32x4 f0[8];
+  u32x4 f1[8];
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    f0[f] = frag(0, 0, f);
+  }
+  for (int kt = 0; kt < nk; ++kt) {
+    const int kc = min(kt + 1, nk - 1);
+    stage_barrier();  // B1: everyone is done with buffer (kt + 1) & 1
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      u32x4(&cur)[8] = (s & 1) ? f1 : f0;
+      u32x4(&nxt)[8] = (s & 1) ? f0 : f1;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        acc[i >> 2][i & 3] = mfma32x32x16<T>(cur[i >> 2], cur[4 + (i & 3)], acc[i >> 2][i & 3]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < 8) {
+          nxt[i] = s < 3 ? frag(kt, s + 1, i) : frag(kt + 1, 0, i);
+        }
+        if (s < 2 && (i & 1)) {
+          issue_one(kc, s * 8 + (i >> 1), kt + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (s == 2) {
+        wait_vmcnt<0>();  // this wave's copies of stage kt + 1 have landed
+        stage_barrier();  // B2: everyone's have
+      }
+    }
+  }
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = bn + wn + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = bm + wm + i * 32 + acc_row(r, lane);
+        if (m < M && n < N) {
+          epi(m, n, acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Ring-pipelined 16-bit TN GEMM for short K (the ViT block's GEMMs, K = 768).
 //
 // With K = 768 a tile has 12 stages of BK = 64 and each stage holds only a
@@ -1504,6 +1656,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 // Tile configurations (block tile BM x BN, waves WM x WN, BK = 64):
 //   w4     256x256, 4 waves 2x2 (128x128 each), ring of 32-deep slices
 //          (gemm_half_tn_w4_kernel); needs A / Bt padded to 256 rows
+//   w4d    256x256, 4 waves 2x2, two 64-deep stages, two barriers per stage
+//          (gemm_half_tn_w4d_kernel); needs A / Bt padded to 256 rows
 //   lds    256x256, 8 waves 2x4 (128x64 each), global -> LDS direct loads
 //          (gemm_half_tn_lds_kernel); needs A / Bt padded to 256 rows
 //   big8   256x256, 8 waves 2x4, LDS double buffer fed from registers
@@ -1511,12 +1665,13 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 //   mid    128x128, 4 waves 2x2 (64x64 each)
 //   small   64x64,  4 waves 2x2 (32x32 each)
 // Default: the largest tile that still gives at least one workgroup per CU
-// (w4 from two tiles per CU and lds below that where the operands are padded,
+// (w4 from two tiles per CU and w4d below that where the operands are padded,
 // big8 elsewhere; measured 8192^3 bf16: w4 1300-1310 against lds 1230-1265
-// TFLOP/s, 4096^3: lds 1245-1260 against w4 1220-1230).
+// TFLOP/s, 4096^3: w4d 1267-1289 against lds 1240-1260 and w4 1220-1230).
+// lds stays selectable (tune cache, CJ_HIP_GEMM_TILE).
 // CJ_HIP_GEMM_TILE=<name> overrides the choice (tuning sweeps), like the
 // reference's CJ_* tuning variables.
-enum class HalfTile { kW4, kLds, kBig8, kBig4, kMid, kSmall };
+enum class HalfTile { kW4, kW4D, kLds, kBig8, kBig4, kMid, kSmall };
 
 inline int tiles_for(int M, int N, int b) { return ((M + b - 1) / b) * ((N + b - 1) / b); }
 
@@ -1524,6 +1679,7 @@ inline HalfTile pick_half_tile(int M, int N, bool padded) {
   if (const char* env = getenv("CJ_HIP_GEMM_TILE")) {
     const std::string v(env);
     if (v == "w4" && padded) return HalfTile::kW4;
+    if (v == "w4d" && padded) return HalfTile::kW4D;
     if (v == "lds" && padded) return HalfTile::kLds;
     if (v == "big8") return HalfTile::kBig8;
     if (v == "big4") return HalfTile::kBig4;
@@ -1535,7 +1691,7 @@ inline HalfTile pick_half_tile(int M, int N, bool padded) {
     return padded ? HalfTile::kW4 : HalfTile::kBig8;
   }
   if (tiles_for(M, N, 256) >= kCUs) {
-    return padded ? HalfTile::kLds : HalfTile::kBig8;
+    return padded ? HalfTile::kW4D : HalfTile::kBig8;
   }
   if (tiles_for(M, N, 128) >= kCUs) {
     return HalfTile::kMid;
@@ -1558,6 +1714,7 @@ static hipError_t launch_gemm_half_tile(HalfTile tile, LoadA load_a, const uint1
                                         int ldb, Epi epi, hipStream_t stream) {
   switch (tile) {
     case HalfTile::kW4:
+    case HalfTile::kW4D:
     case HalfTile::kLds:
     case HalfTile::kBig8:
       return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
@@ -1596,13 +1753,18 @@ inline bool vit_ring_enabled() {
 // Its copies use 32-bit byte offsets from a stage base and 16-byte alignment.
 inline bool ring_fits(long long rows, long long ld) { return rows * ld * 2 < (1LL << 31) && ld % 8 == 0; }
 
-template <typename T>
+template <typename T, bool DOUBLE>
 static hipError_t launch_gemm_w4(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda,
                                  int ldb, int ldc, hipStream_t stream) {
   const int tiles_n = (N + 255) / 256;
   const dim3 grid(((M + 255) / 256) * tiles_n);
-  hipLaunchKernelGGL((gemm_half_tn_w4_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
-                     tiles_n, EpiF32{C, ldc});
+  if constexpr (DOUBLE) {
+    hipLaunchKernelGGL((gemm_half_tn_w4d_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
+                       tiles_n, EpiF32{C, ldc});
+  } else {
+    hipLaunchKernelGGL((gemm_half_tn_w4_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
+                       tiles_n, EpiF32{C, ldc});
+  }
   return hipGetLastError();
 }
 
@@ -1693,6 +1855,7 @@ GemmHalfVariant gemmHalfChoose(int M, int N) {
   }
   switch (pick_half_tile(M, N, true)) {
     case HalfTile::kW4: return GemmHalfVariant::kW4;
+    case HalfTile::kW4D: return GemmHalfVariant::kW4D;
     case HalfTile::kLds: return GemmHalfVariant::kLds;
     case HalfTile::kBig8: return GemmHalfVariant::kBig8;
     case HalfTile::kBig4: return GemmHalfVariant::kBig4;
@@ -1714,13 +1877,17 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
   }
   // A and Bt come from the resident upload, padded to 256 rows; the copies'
   // 32-bit lane offsets reach 256 rows of either operand.
-  if ((variant == GemmHalfVariant::kLds || variant == GemmHalfVariant::kW4) &&
+  if ((variant == GemmHalfVariant::kLds || variant == GemmHalfVariant::kW4 || variant == GemmHalfVariant::kW4D) &&
       (256LL * lda * 2 >= (1LL << 31) || 256LL * ldb * 2 >= (1LL << 31))) {
     variant = GemmHalfVariant::kBig8;
   }
   if (variant == GemmHalfVariant::kW4 && K > 0) {
-    return t == Half::kBF16 ? launch_gemm_w4<BF16>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
-                            : launch_gemm_w4<F16>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
+    return t == Half::kBF16 ? launch_gemm_w4<BF16, false>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
+                            : launch_gemm_w4<F16, false>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
+  }
+  if (variant == GemmHalfVariant::kW4D && K > 0) {
+    return t == Half::kBF16 ? launch_gemm_w4<BF16, true>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
+                            : launch_gemm_w4<F16, true>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
   }
   if (variant == GemmHalfVariant::kLds && K > 0) {
     return t == Half::kBF16 ? launch_gemm_lds<BF16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
