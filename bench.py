@@ -1,18 +1,19 @@
 """Benchmark: attention2d & matmul2d TFLOP/s (+% of MFMA peak) on 1 MI355X vs host CPU.
 
-Headline workload: matmul2d fp32, one step = one
-1024^3 GEMM plus one 1000x1030x777 GEMM, inputs resident in HBM (uploaded
-once through resident sessions), launch-only.  `value` = algorithmic FLOPs of
-the timed steps / wall time of the timed region (hipEvents on the backend
-stream, device synchronised on both sides).
+Headline workload: BASELINE.json configs[4], the largest single-GPU config:
+matmul2d bf16 (fp32 accumulate, fp32 C) M=N=K=8192 in a resident session,
+inputs uploaded and converted once, then launch-only.  One step = one
+8192^3 GEMM launch; the default times the config's 100 iterations.  `value` =
+algorithmic FLOPs (2*M*N*K per step) / wall time of the timed region
+(hipEvents on the backend stream, device synchronised on both sides).
+`roofline` is the dominant kernel, gemm_half_tn_w4_kernel, whose average
+launch time is measured the same way; `cpu_baseline` is the reference's own
+matMulCpu (oracle/_ref/libref.so, single thread) on a row subset of the same
+bf16-rounded operands, scaled by rows (output rows are independent).
 
 Also reported (`per_config`): every other BASELINE config on its own resident
 launch-only loop, each with TFLOP/s (or GB/s for the HBM-bound skinny GEMM)
 and its fraction of the gfx950 peak, plus a bounded CPU-baseline sample.
-
-The CPU baseline runs the reference's own CPU path (oracle/_ref/libref.so,
-compiled from the reference sources) when present, else this build's C
-restatement (oracle/liboracle.so), single-threaded, on a bounded sample.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-extras]
 """
@@ -161,12 +162,85 @@ def cpu_threads_used():
     return 1
 
 
+def host_record():
+    """CPU model and thread counts of the host the CPU baseline runs on."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 0
+    return {"cpu_model": model, "nproc": usable, "cpu_count": os.cpu_count()}
+
+
 # ---------------------------------------------------------------------------
 # workloads
 # ---------------------------------------------------------------------------
 
-def bench_config2(lc, synth, steps, warmup, cpu):
-    """Headline: fp32 GEMM 1024^3 + 1000x1030x777."""
+HEADLINE = (8192, 8192, 8192)
+# CPU baseline of the headline: rows of C in chunks until this much CPU time
+CPU_SAMPLE_S = 12.0
+
+
+def bench_headline(lc, synth, steps, warmup, cpu):
+    """configs[4] at 8192^3: bf16 GEMM, resident session, launch-only."""
+    m, k, n = HEADLINE
+    a = synth.normal((m, k), stream=230)
+    b = synth.normal((k, n), stream=231)
+    sess = lc.MatMulResidentSession(m, k, n, "bf16")
+    sess.start_into(a, b)
+    lc.device_synchronize()
+    flops_step = 2.0 * m * k * n
+
+    def step_loop(iters):
+        if iters > 0:
+            sess.run_batch_sync_cached_no_download(iters)
+
+    step_loop(warmup)
+    ms = timed(lc, step_loop, steps)
+    ms_per_step = ms / steps
+    value = flops_step / (ms_per_step * 1e-3) / 1e12
+    # the dominant (only) kernel of a step: its average launch time over the
+    # same back-to-back loop, measured on the backend stream
+    kms = ms_per_step
+    achieved = flops_step / (kms * 1e-3) / 1e12
+    roofline = {"bound": "mfma", "kernel": "gemm_half_tn_w4_kernel<BF16> (8192^3, v_mfma_f32_32x32x16_bf16)",
+                "achieved": round(achieved, 3), "peak": PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_TFLOPS["bf16"], 4), "traffic": GEMM_BF16_8192_TRAFFIC,
+                "avg_kernel_ms": round(kms, 5), "algorithmic_flops_per_launch": int(flops_step),
+                "algorithmic_bytes_per_launch": m * k * 2 + k * n * 2 + m * n * 4}
+    cpu_obj = None
+    if cpu.kind is not None:
+        log(f"[bench] cpu baseline ({cpu.kind}) on config 5 8192^3 rows ...")
+        ar, br = synth.round_bf16(a), synth.round_bf16(b)
+        chunk = 8
+        t0 = time.perf_counter()
+        rows = 0
+        while rows < m:
+            cpu.matmul(np.ascontiguousarray(ar[rows:rows + chunk]), br)
+            rows += chunk
+            el = time.perf_counter() - t0
+            if el >= CPU_SAMPLE_S:
+                break
+        el = time.perf_counter() - t0
+        cpu_tf = 2.0 * rows * k * n / el / 1e12
+        cpu_obj = {"value": round(cpu_tf, 6), "unit": "TFLOP/s", "cores": cpu_threads_used(), "kind": cpu.kind,
+                   "sample": f"{rows} of {m} rows of C (8192^3 GEMM on the bf16-rounded operands promoted to fp32) "
+                             f"in {el:.1f} s, single thread, -O3 -ffast-math -funroll-loops; rows are independent, "
+                             f"so the full GEMM would take x{m / rows:.0f}: {el * m / rows:.0f} s"}
+    sess.close()
+    return value, ms_per_step, roofline, cpu_obj
+
+
+def bench_config2(lc, synth, cpu):
+    """fp32 GEMM 1024^3 + 1000x1030x777 per step, resident, launch-only."""
     shapes = [(1024, 1024, 1024), (1000, 777, 1030)]
     sess, inputs = [], []
     for i, (m, k, n) in enumerate(shapes):
@@ -184,25 +258,21 @@ def bench_config2(lc, synth, steps, warmup, cpu):
             for s in sess:
                 s.run_into()
 
-    step_loop(warmup)
-    ms = timed(lc, step_loop, steps)
-    ms_per_step = ms / steps
-    value = flops_step / (ms_per_step * 1e-3) / 1e12
-
-    # dominant kernel (1024^3 GEMM) alone, back-to-back launches
-    reps = max(50, steps)
+    steps = 50
+    step_loop(10)
+    ms_per_step = timed(lc, step_loop, steps) / steps
+    # the 1024^3 GEMM alone, back-to-back launches
+    reps = 50
     sess[0].run_batch_sync_cached_no_download(5)
     kms = timed(lc, lambda it: sess[0].run_batch_sync_cached_no_download(it), reps) / reps
     kflops = 2.0 * 1024 ** 3
     achieved = kflops / (kms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "gemm_f32_lds_kernel<64,2,2> (1024^3, v_mfma_f32_32x32x2_f32)",
-                "achieved": round(achieved, 3), "peak": PEAK_TFLOPS["f32"], "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_TFLOPS["f32"], 4), "traffic": GEMM_F32_1024_TRAFFIC,
-                "avg_kernel_ms": round(kms, 5), "algorithmic_flops_per_launch": int(kflops)}
-
-    cpu_obj = None
+    entry = extra_entry("C2", flops_step, ms_per_step, "f32")
+    entry["kernel_1024^3"] = {"kernel": "gemm_f32_lds_kernel<64,2,2> (v_mfma_f32_32x32x2_f32)",
+                              "avg_kernel_ms": round(kms, 5), "TFLOP/s": round(achieved, 3),
+                              "frac_peak": round(achieved / PEAK_TFLOPS["f32"], 4),
+                              "traffic": GEMM_F32_1024_TRAFFIC}
     if cpu.kind is not None:
-        log(f"[bench] cpu baseline ({cpu.kind}) on config 2 ...")
         t0 = time.perf_counter()
         reps_done, flops_done = 0, 0.0
         while True:
@@ -211,16 +281,13 @@ def bench_config2(lc, synth, steps, warmup, cpu):
                 flops_done += 2.0 * m * k * n
             reps_done += 1
             el = time.perf_counter() - t0
-            if el >= 10.0 or reps_done >= 30:
+            if el >= 3.0 or reps_done >= 30:
                 break
-        cpu_obj = {"value": round(flops_done / el / 1e12, 6), "unit": "TFLOP/s", "cores": cpu_threads_used(),
-                   "kind": cpu.kind,
-                   "sample": f"{reps_done} full steps (1024^3 + 1000x1030x777 fp32 GEMM) in {el:.1f} s, "
-                             "single thread, -O3 -ffast-math -funroll-loops"}
-    # free device memory before the large extras
+        entry["cpu_TFLOP/s"] = round(flops_done / el / 1e12, 6)
+        entry["cpu_sample"] = f"{reps_done} full steps in {el:.1f} s, 1 thread ({cpu.kind})"
     for s in sess:
         s.close()
-    return value, ms_per_step, roofline, cpu_obj
+    return entry
 
 
 def extra_entry(name, flops, ms, dtype, cpu_tflops=None, cpu_sample=None, bytes_=None, bound="mfma"):
@@ -242,7 +309,7 @@ def extra_entry(name, flops, ms, dtype, cpu_tflops=None, cpu_sample=None, bytes_
 
 
 def bench_extras(lc, synth, cpu):
-    out = {}
+    out = {"C2_gemm_f32_1024^3_plus_1000x1030x777": bench_config2(lc, synth, cpu)}
     # C1 attention fp32 S=256 D=64
     s, d = 256, 64
     q, k, v = (synth.normal((s, d), stream=200 + i) for i in range(3))
@@ -385,8 +452,8 @@ def bench_extras(lc, synth, cpu):
     out["C4_vit_block_f16_B8"] = extra_entry("C4", flops, ms, "f16", cpu_tf, sample)
     vs.close()
 
-    # C5 bf16 GEMM sweep, 100 launches in a resident session
-    for m, k, n in ((4096, 4096, 4096), (8192, 8192, 8192), (16, 8192, 8192)):
+    # C5 bf16 GEMM sweep, 100 launches in a resident session (8192^3 is the headline)
+    for m, k, n in ((4096, 4096, 4096), (16, 8192, 8192)):
         a = synth.normal((m, k), stream=230)
         bm = synth.normal((k, n), stream=231)
         sess = lc.MatMulResidentSession(m, k, n, "bf16")
@@ -426,6 +493,8 @@ PMC_GEMMS = 20
 # FETCH_SIZE: GEMM 12329.9 KiB/dispatch, copy 131084.4 KiB for 262144 KiB moved (x2.000);
 # WRITE_SIZE: GEMM 4096.0 KiB/dispatch, copy 262144.0 KiB (x1.000).
 GEMM_F32_1024_TRAFFIC = 25235186 + 4194304  # HBM bytes per launch (fetch + write, calibrated)
+# 8192^3 bf16 (gemm_half_tn_w4_kernel), profiles/gemm_half_tn_w4_kernel_8192cube_traffic.txt
+GEMM_BF16_8192_TRAFFIC = None
 
 
 def pmc_workload(lc, synth, which="c2"):
@@ -441,6 +510,16 @@ def pmc_workload(lc, synth, which="c2"):
     finally:
         lib.lcFree(src)
         lib.lcFree(dst)
+    if which == "c5":
+        m = HEADLINE[0]
+        s = lc.MatMulResidentSession(m, m, m, "bf16")
+        s.start_into(synth.normal((m, m), stream=230), synth.normal((m, m), stream=231))
+        s.run_batch_sync_cached_no_download(PMC_GEMMS)
+        lc.device_synchronize()
+        s.close()
+        log(f"[bench] pmc workload done: {PMC_COPIES} copies of {PMC_COPY_BYTES} bytes, 1 + {PMC_GEMMS} launches "
+            f"of the {m}^3 bf16 GEMM (the first from the session start)")
+        return
     if which == "c2":
         a = synth.uniform((1024, 1024), stream=100)
         b = synth.uniform((1024, 1024), stream=101)
@@ -481,14 +560,14 @@ def pmc_workload(lc, synth, which="c2"):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--pmc-workload", nargs="?", const="c2", default=None, choices=("c2", "bf16"),
+    ap.add_argument("--pmc-workload", nargs="?", const="c5", default=None, choices=("c5", "c2", "bf16"),
                     help="run only the fixed workload the rocprofv3 --pmc passes count: "
                          f"{PMC_COPIES} device-to-device copies of {PMC_COPY_BYTES >> 20} MiB (calibration), "
-                         f"then {PMC_GEMMS} launches of the 1024^3 fp32 GEMM (c2, the default) or a few launches "
-                         "of each 16-bit config (bf16)")
+                         f"then {PMC_GEMMS} launches of the 8192^3 bf16 GEMM (c5, the default), of the 1024^3 "
+                         "fp32 GEMM (c2), or a few launches of each 16-bit config (bf16)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         log("bench.py: this build measures one GPU only (the path is single-GPU; see DESIGN.md for how it would "
@@ -507,8 +586,8 @@ def main():
         pmc_workload(lc, synth, args.pmc_workload)
         return
     cpu = CpuBaseline()
-    value, ms_per_step, roofline, cpu_obj = bench_config2(lc, synth, args.steps, args.warmup, cpu)
-    log(f"[bench] config2: {value:.3f} TFLOP/s, {ms_per_step:.4f} ms/step, kernel {roofline}")
+    value, ms_per_step, roofline, cpu_obj = bench_headline(lc, synth, args.steps, args.warmup, cpu)
+    log(f"[bench] config5 8192^3: {value:.3f} TFLOP/s, {ms_per_step:.4f} ms/step, kernel {roofline}")
     extras = {} if args.no_extras else bench_extras(lc, synth, cpu)
     line = {
         "metric": METRIC,
@@ -522,12 +601,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic: SplitMix64 U(-1,1), seed 20260401, inputs resident in HBM",
-        "config": {"workload": "configs[1]: matmul2d fp32 GEMM 1024x1024x1024 + 1000x1030x777 per step, "
-                               "resident sessions, launch-only",
+        "dtype": "bf16",
+        "data": "synthetic: SplitMix64 N(0,1) rounded to bf16 (RNE), seed 20260401, inputs resident in HBM",
+        "config": {"workload": "configs[4]: matmul2d bf16 GEMM M=N=K=8192 (fp32 accumulate, fp32 C), resident "
+                               "session (upload once), launch-only, one launch per step",
                    "parallelism": "single GPU", "device": info["name"], "arch": info["gcn_arch"],
-                   "compute_units": info["compute_units"]},
+                   "compute_units": info["compute_units"], "max_clock_khz": info["max_clock_khz"],
+                   "host": host_record()},
         "roofline": roofline,
         "cpu_baseline": cpu_obj,
         "per_config": extras,

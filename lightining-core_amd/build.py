@@ -43,6 +43,12 @@ def _compile(src: str) -> str:
     err = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if noise not in l)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {src}\n{err}")
+    # Inline asm must never clobber a register the compiler reserves (M0,
+    # EXEC, VCC, ...): the compiler neither saves nor restores it, so a live
+    # value it keeps there would be silently corrupted.  Such registers are
+    # passed as operands ("{m0}") instead; the warning is a build error here.
+    if "Reserved registers on the clobber list" in err:
+        raise RuntimeError(f"inline asm clobbers a reserved register: {src}\n{err}")
     if err.strip():
         print(err, file=sys.stderr)
     return obj

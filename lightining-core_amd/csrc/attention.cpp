@@ -158,6 +158,7 @@ Status forwardSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, co
                      int* splits) {
   AttnTuneKey key;
   key.kind = 'F';
+  key.arch = baseArch(ctx);
   key.seq = sh.seq_len;
   key.dim = sh.head_dim;
   key.causal = sh.causal ? 1 : 0;
@@ -194,6 +195,7 @@ Status trainSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, cons
                    bool compute_loss, float lr, int* splits) {
   AttnTuneKey key;
   key.kind = 'T';
+  key.arch = baseArch(ctx);
   key.seq = sh.seq_len;
   key.dim = sh.head_dim;
   key.causal = sh.causal ? 1 : 0;

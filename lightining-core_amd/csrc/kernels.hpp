@@ -25,19 +25,34 @@ constexpr int kF32GemmBK = 64;    // K multiple (zero-padded)
 // C[M,N] = A[M,K] . B[K,N] (row-major, leading dimensions lda/ldb/ldc), any sizes.
 hipError_t gemmF32(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
                    hipStream_t stream);
+// Workspace and protocol state of the stream-K fp32 GEMM.  `part` holds
+// max_groups * 4096 floats of partial tiles and `flags` max_groups ints;
+// a workgroup publishes its partial by storing `epoch` to its flag, so the
+// caller passes a value no earlier launch over the same flags used (flags
+// start at zero; epochs from 1).  Owners poll a flag at most `spin_limit`
+// times; one whose wait runs out stores 1 to *fail (device-visible memory the
+// caller clears and checks after the stream sync) and that launch's result
+// is invalid.  Launches that share part/flags must not overlap.
+struct StreamKSync {
+  float* part;
+  int* flags;
+  int* fail;
+  int epoch;
+  int spin_limit;
+};
+// Default bound of a stream-K owner's wait (polls of ~0.25 us each).
+constexpr int kStreamKSpinLimit = 1 << 22;
 // Same product on padded operands: A [roundup(M,64), K] (lda), B [K,
 // roundup(N,64)] (ldb), K a multiple of kF32GemmBK, pads zero, lda/ldb
 // multiples of 4 and both bases 16-byte aligned.  C [M, N] (ldc).  Stream-K
-// over at most max_groups workgroups: `part` holds max_groups * 4096 floats
-// of partial tiles and `flags` max_groups ints, zero before the first call
-// (each call leaves them zero).  Calls that share part/flags must not overlap.
+// over at most max_groups workgroups with the workspace in `sync`.
 // Variants: whole 64x64 tiles per workgroup (BK 64 or 32), or stream-K
 // (BK 64); kAuto takes CJ_HIP_GEMM_F32=dp|sk|bk32, else the heuristic of
 // gemmF32Choose.
 enum class GemmF32Variant { kAuto = 0, kDataParallel = 1, kStreamK = 2, kDataParallelBK32 = 3 };
 GemmF32Variant gemmF32Choose(int M, int N, int max_groups);
 hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
-                         float* part, int* flags, int max_groups, GemmF32Variant variant, hipStream_t stream);
+                         const StreamKSync& sync, int max_groups, GemmF32Variant variant, hipStream_t stream);
 // dst[r][c] = src[r][c] (row stride ld_src) for r < rows, c < cols; 0 up to
 // rows_pad x cols_pad (dst row stride cols_pad).
 hipError_t padCopyF32(const float* src, float* dst, int rows, int cols, size_t ld_src, int rows_pad, int cols_pad,

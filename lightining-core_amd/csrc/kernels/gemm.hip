@@ -21,6 +21,8 @@
 
 namespace lchip::k {
 
+using kern::StreamKSync;
+
 // ---------------------------------------------------------------------------
 // fp32
 // ---------------------------------------------------------------------------
@@ -1339,16 +1341,21 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, 
 // workgroup walks its range downwards, so the first segment it finishes is
 // the low-k part of its last tile and the last segment the high-k part of
 // its first tile.  A segment without the tile's last k stage publishes its
-// partial tile (part[w], flag[w] = 1) as soon as it is done; the segment
+// partial tile (part[w], flag[w] = epoch) as soon as it is done; the segment
 // holding the last stage owns the tile: it waits for the flags of the lower
 // workgroups that hold the rest, adds their partials in workgroup order
 // (deterministic) and stores.  With xl set, each XCD's workgroups split only
 // the iterations of that XCD's own contiguous range of tiles (the same
 // protocol among the ranks of one XCD).  Waits only ever target lower workgroup ids,
-// which the in-order dispatch has already started, and each spin is bounded,
-// so every wave exits.  With T a multiple of G (1024^3: 256 tiles on 256
-// CUs) every range is whole tiles and nothing is published.  The owner
-// clears the flags it consumed, so they are zero again when the kernel ends.
+// which the in-order dispatch has already started, and each wait polls at
+// most spin_limit times, so every wave exits.  An owner whose wait runs out
+// stores 1 to *fail (the host turns it into an error after the stream sync)
+// and stops waiting: that launch's result is invalid.  Flags carry the
+// launch's epoch, a number the host changes on every launch, so a flag left
+// by an earlier launch (one whose owner gave up before a late publisher set
+// it) never reads as ready; flags are never cleared.  With T a multiple of G
+// (1024^3: 256 tiles on 256 CUs) every range is whole tiles and nothing is
+// published.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
@@ -1358,8 +1365,7 @@ __device__ __forceinline__ void lds_barrier() {
 template <int BK, int STAGES, int KS, bool SK, typename Epi>
 __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                            int M, int N, int lda, int ldb, int tiles_m, int tiles_n,
-                                                           int nk, float* __restrict__ part, int* __restrict__ flags,
-                                                           Epi epi, int xl = 0) {
+                                                           int nk, StreamKSync sync, Epi epi, int xl = 0) {
   constexpr int BM = 64, BN = 64;
   constexpr int A_STAGE = BM * BK;            // floats
   constexpr int STAGE = (BM + BN) * BK;       // floats
@@ -1508,7 +1514,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
     // the XCD and cost every other workgroup there its cached A / B tiles.
     // Order comes from waiting for the partial stores to complete (vmcnt)
     // before the flag store, and from the barrier after the flag spin.
-    float* mine = part + static_cast<size_t>(w) * 4096 + sub * 1024 + lane;
+    float* mine = sync.part + static_cast<size_t>(w) * 4096 + sub * 1024 + lane;
     if (!has_last) {
       if (kh == 0) {
 #pragma unroll
@@ -1519,7 +1525,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
       wait_vmcnt<0>();
       stage_barrier();
       if (tid == 0) {
-        __hip_atomic_store(flags + w, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sync.flags + w, sync.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       return;
     }
@@ -1536,27 +1542,28 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
           if (begin_of(q) == begin_of(q + 1)) {
             continue;
           }
-          for (int spin = 0; spin < (1 << 22); ++spin) {
-            if (__hip_atomic_load(flags + wg_of(q), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) {
-              break;
-            }
+          const int* flag = sync.flags + wg_of(q);
+          int spin = 0;
+          while (spin < sync.spin_limit &&
+                 __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != sync.epoch) {
             __builtin_amdgcn_s_sleep(4);
+            ++spin;
+          }
+          if (spin >= sync.spin_limit) {
+            // gave up: report, and wait for no further partial
+            __hip_atomic_store(sync.fail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            break;
           }
         }
       }
       stage_barrier();
       if (kh == 0) {
         for (int q = wf; q < rank; ++q) {
-          float* theirs = part + static_cast<size_t>(wg_of(q)) * 4096 + sub * 1024 + lane;
+          float* theirs = sync.part + static_cast<size_t>(wg_of(q)) * 4096 + sub * 1024 + lane;
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             v[i] += __hip_atomic_load(theirs + i * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
-        }
-      }
-      if (tid == 0) {
-        for (int q = wf; q < rank; ++q) {
-          __hip_atomic_store(flags + wg_of(q), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
     }
@@ -1804,7 +1811,7 @@ GemmF32Variant gemmF32Choose(int M, int N, int max_groups) {
 }
 
 hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N, int K, int lda, int ldb, int ldc,
-                         float* part, int* flags, int max_groups, GemmF32Variant variant, hipStream_t stream) {
+                         const StreamKSync& sync, int max_groups, GemmF32Variant variant, hipStream_t stream) {
   if (K <= 0 || K % kF32GemmBK != 0 || lda % 4 != 0 || ldb % 4 != 0 || M <= 0 || N <= 0 || max_groups <= 0) {
     return hipErrorInvalidValue;
   }
@@ -1827,7 +1834,7 @@ hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N,
   const EpiStoreF32 epi{C, ldc};
   if (bk32) {
     hipLaunchKernelGGL((gemm_f32_lds_kernel<32, 4, 2, false, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A,
-                       B, M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi, 0);
+                       B, M, N, lda, ldb, tiles_m, tiles_n, nk, sync, epi, 0);
   } else if (sk) {
     // Two stages (80 KB of LDS): measured fastest on every shape tried
     // (1024^3 to 4096x4096x1024, stream-K and whole tiles): a shorter
@@ -1837,10 +1844,10 @@ hipError_t gemmF32Padded(const float* A, const float* B, float* C, int M, int N,
     // scatter over its range: 1500^3 71.6 -> 77.4 us, so the global order stays).
     const int xl = (groups % 8 == 0 && tiles >= 8 && tiles < 2 * groups) ? 1 : 0;
     hipLaunchKernelGGL((gemm_f32_lds_kernel<64, 2, 2, true, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A, B,
-                       M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi, xl);
+                       M, N, lda, ldb, tiles_m, tiles_n, nk, sync, epi, xl);
   } else {
     hipLaunchKernelGGL((gemm_f32_lds_kernel<64, 2, 2, false, EpiStoreF32>), dim3(groups), dim3(512), 0, stream, A, B,
-                       M, N, lda, ldb, tiles_m, tiles_n, nk, part, flags, epi, 0);
+                       M, N, lda, ldb, tiles_m, tiles_n, nk, sync, epi, 0);
   }
   return hipGetLastError();
 }

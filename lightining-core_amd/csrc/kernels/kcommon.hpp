@@ -124,10 +124,12 @@ __device__ __forceinline__ floatx16 zero16() {
 //    compiler-visible global -> LDS copy makes every later LDS wait an
 //    lgkmcnt(0), which stalls each MFMA group on LDS reads issued for the
 //    next one.  Callers wait for these copies with explicit vmcnt.
-// `lds` and `sbase` must be wave-uniform; M0 is clobbered.
+// `lds` and `sbase` must be wave-uniform.  The LDS address reaches M0 through
+// an "{m0}" input operand, so the compiler itself writes M0 (and knows its
+// value afterwards); the asm never writes M0.  The s_nop covers the one wait
+// state an M0 write needs before an LDS-DMA load reads it.
 __device__ __forceinline__ void load_lds16_sbase(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds)
-               : "memory", "m0");
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
 }
 
 // LDS byte address of a __shared__ object, as a wave-uniform value.

@@ -128,8 +128,13 @@ struct HipContext {
   PinnedBuffer pinned;
   // Stream-K workspace of the fp32 GEMM (partial tiles + ready flags), one
   // slot per workgroup; used by launches on `stream` only, so never shared
-  // by two kernels at once.
+  // by two kernels at once.  Each launch publishes with a new epoch
+  // (nextStreamKEpoch).  gemm_fail is a pinned, device-mapped word an owner
+  // sets when its bounded wait for a partial tile runs out; syncStream turns
+  // it into an error.
   DeviceBuffer gemm_part, gemm_flags;
+  PinnedBuffer gemm_fail;
+  int gemm_epoch = 0;
 };
 
 bool hipAvailable();
@@ -140,8 +145,22 @@ HipContext* hipContext(Status* st);
 // Upload / download on the context stream (pageable host memory).
 Status upload(HipContext* ctx, void* dst, const void* src, std::size_t bytes);
 Status download(HipContext* ctx, void* dst, const void* src, std::size_t bytes);
+// Synchronises the backend stream, then reports a failure a kernel recorded
+// since the last sync (a stream-K wait that ran out) as kDriverError.
 Status syncStream(HipContext* ctx);
+// The epoch for the next stream-K launch over gemm_flags (clears the flags
+// on the stream when the counter wraps).
+Status nextStreamKEpoch(HipContext* ctx, int* epoch);
+// CJ_HIP_STREAMK_SPIN_LIMIT (polls, >= 0), else kern::kStreamKSpinLimit.
+int streamKSpinLimit();
 
 inline std::size_t roundUp(std::size_t v, std::size_t m) { return (v + m - 1) / m * m; }
+
+// The device's base architecture ("gfx950"), without the target features
+// after ':' -- the arch column of the tune caches.
+inline std::string baseArch(const HipContext* ctx) {
+  const std::string arch = ctx->props.gcnArchName;
+  return arch.substr(0, arch.find(':'));
+}
 
 }  // namespace lchip

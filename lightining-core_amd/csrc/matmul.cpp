@@ -152,12 +152,21 @@ hipError_t launchGemm(HipContext* ctx, MatMulResident& r, int variant) {
     const int np = static_cast<int>(roundUp(r.n, kern::kF32GemmBN));
     // stream-K: one workgroup per CU (a whole-tile grid may hold two per CU)
     const int groups = ctx->props.multiProcessorCount > 0 ? ctx->props.multiProcessorCount : 256;
+    const bool fresh_fail = ctx->gemm_fail.get() == nullptr;
     if (ctx->gemm_part.ensure(static_cast<std::size_t>(groups) * 4096 * sizeof(float)) != Status::kSuccess ||
-        ctx->gemm_flags.ensure(static_cast<std::size_t>(groups) * sizeof(int), true) != Status::kSuccess) {
+        ctx->gemm_flags.ensure(static_cast<std::size_t>(groups) * sizeof(int), true) != Status::kSuccess ||
+        ctx->gemm_fail.ensure(sizeof(int)) != Status::kSuccess) {
       return hipErrorOutOfMemory;
     }
-    return kern::gemmF32Padded(r.a.as<float>(), r.b.as<float>(), r.c.as<float>(), M, N, kp, kp, np, N,
-                               ctx->gemm_part.as<float>(), ctx->gemm_flags.as<int>(), groups,
+    if (fresh_fail) {
+      *static_cast<int*>(ctx->gemm_fail.get()) = 0;
+    }
+    kern::StreamKSync sync{ctx->gemm_part.as<float>(), ctx->gemm_flags.as<int>(),
+                           static_cast<int*>(ctx->gemm_fail.device()), 0, streamKSpinLimit()};
+    if (nextStreamKEpoch(ctx, &sync.epoch) != Status::kSuccess) {
+      return hipErrorUnknown;
+    }
+    return kern::gemmF32Padded(r.a.as<float>(), r.b.as<float>(), r.c.as<float>(), M, N, kp, kp, np, N, sync, groups,
                                static_cast<kern::GemmF32Variant>(variant), ctx->stream);
   }
   const int kp = static_cast<int>(roundUp(r.k, kern::kHalfGemmBK));
@@ -218,9 +227,7 @@ Status settleVariant(HipContext* ctx, MatMulResident& r) {
   if (std::getenv(half ? "CJ_HIP_GEMM_TILE" : "CJ_HIP_GEMM_F32") != nullptr) {
     return Status::kSuccess;
   }
-  // base architecture ("gfx950"), without the target features after ':'
-  std::string arch = ctx->props.gcnArchName;
-  arch = arch.substr(0, arch.find(':'));
+  const std::string arch = baseArch(ctx);
   const int dtype = static_cast<int>(r.dtype);
   TuneEntry known;
   if (tuneLookup(r.m, r.k, r.n, dtype, arch, &known) && variantFromEntry(known, half, r.m, &r.variant)) {

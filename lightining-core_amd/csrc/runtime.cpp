@@ -14,9 +14,11 @@
 #include <atomic>
 #include <chrono>
 #include <cstdarg>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
+#include "kernels.hpp"
 #include "lc_internal.hpp"
 #include "tune.hpp"
 
@@ -252,7 +254,35 @@ Status download(HipContext* ctx, void* dst, const void* src, std::size_t bytes) 
 
 Status syncStream(HipContext* ctx) {
   LC_HIP_TRY(hipStreamSynchronize(ctx->stream));
+  if (int* word = static_cast<int*>(ctx->gemm_fail.get())) {
+    if (__atomic_exchange_n(word, 0, __ATOMIC_ACQ_REL) != 0) {
+      return fail(Status::kDriverError,
+                  "matmul: a stream-K workgroup's bounded wait for a partial tile ran out "
+                  "(CJ_HIP_STREAMK_SPIN_LIMIT); the result of that launch is invalid");
+    }
+  }
   return Status::kSuccess;
+}
+
+Status nextStreamKEpoch(HipContext* ctx, int* epoch) {
+  if (ctx->gemm_epoch >= (1 << 30)) {
+    // wrap: no flag may still hold an epoch the new sequence reuses
+    LC_HIP_TRY(hipMemsetAsync(ctx->gemm_flags.get(), 0, ctx->gemm_flags.size(), ctx->stream));
+    ctx->gemm_epoch = 0;
+  }
+  *epoch = ++ctx->gemm_epoch;
+  return Status::kSuccess;
+}
+
+int streamKSpinLimit() {
+  if (const char* env = std::getenv("CJ_HIP_STREAMK_SPIN_LIMIT")) {
+    char* end = nullptr;
+    const long v = std::strtol(env, &end, 10);
+    if (end != env && *end == '\0' && v >= 0 && v <= (1L << 30)) {
+      return static_cast<int>(v);
+    }
+  }
+  return kern::kStreamKSpinLimit;
 }
 
 // ---------------------------------------------------------------------------

@@ -7,12 +7,14 @@
 // version 2 is written; a header of another kind or version clears the table
 // (the reference re-tunes then).  Rows are re-keyed for gfx950:
 //   matmul    m,k,n,dtype,arch,kernel,tile_m,tile_n,tile_k,waves,split_k
-//   attention kind,seq,dim,causal,resident_hint,sync_hint,[compute_loss,]mode
-// Matmul rows in the reference's own layouts (5 or 6 columns, Metal tiles)
-// mean nothing on gfx950; they are kept verbatim and written back so a file
-// shared with the reference keeps its rows.  The attention layout is the
-// reference's; its mode is the gfx950 split count (1, 2, 4, 8), and a row
-// whose mode is not one of those is dropped.
+//   attention HF|HT,seq,dim,causal,resident_hint,sync_hint,[compute_loss,]arch,splits
+// Rows in the reference's own layouts (matmul: 5 or 6 columns, Metal tiles;
+// attention: F / T rows whose mode is a Metal forward / train mode) mean
+// nothing on gfx950; they are kept verbatim and written back so a file
+// shared with the reference keeps its rows.  gfx950 attention rows use their
+// own kinds (HF forward, HT train step), which the reference's reader skips,
+// and carry the arch; the value is the fp32 kernel's split count (1, 2, 4, 8),
+// and a row whose value is not one of those is dropped.
 //
 // The runtime profile autoload restates src/runtime.cpp:101-168.
 #include <algorithm>
@@ -215,15 +217,17 @@ bool sameEntry(const TuneEntry& a, const TuneEntry& b) {
 // ---------------------------------------------------------------------------
 // attention
 // ---------------------------------------------------------------------------
-using AKey = std::tuple<char, std::size_t, std::size_t, int, int, int, int>;
+using AKey = std::tuple<char, std::size_t, std::size_t, int, int, int, int, std::string>;
 
 AKey akey(const AttnTuneKey& k) {
-  return AKey{k.kind, k.seq, k.dim, k.causal, k.resident_hint, k.sync_hint, k.kind == 'T' ? k.compute_loss : 0};
+  return AKey{k.kind, k.seq, k.dim, k.causal, k.resident_hint, k.sync_hint, k.kind == 'T' ? k.compute_loss : 0,
+              k.arch};
 }
 
 struct AttnCache {
   std::mutex mu;
   std::map<AKey, int> table;
+  std::vector<std::string> foreign;  // reference-layout F / T rows, kept verbatim
   bool loaded = false;
   std::string path;
 };
@@ -234,10 +238,20 @@ AttnCache& at() {
 }
 
 const char* kAttnColumns = "#columns,kind,seq,dim,causal,resident_hint,sync_hint,compute_loss_or_mode,mode";
+const char* kAttnHipColumns = "#columns_hip,kind,seq,dim,causal,resident_hint,sync_hint,compute_loss(HT),arch,splits";
 
 bool validSplit(int mode) { return mode == 1 || mode == 2 || mode == 4 || mode == 8; }
 
-bool parseAttn(const std::string& path, std::map<AKey, int>* table, bool* opened) {
+std::string joinCsv(const std::vector<std::string>& c) {
+  std::string joined;
+  for (std::size_t i = 0; i < c.size(); ++i) {
+    joined += (i ? "," : "") + c[i];
+  }
+  return joined;
+}
+
+bool parseAttn(const std::string& path, std::map<AKey, int>* table, std::vector<std::string>* foreign,
+               bool* opened) {
   bool header_ok = true;
   std::vector<std::vector<std::string>> rows;
   *opened = readCacheFile(path, "attention", &header_ok, &rows);
@@ -249,18 +263,20 @@ bool parseAttn(const std::string& path, std::map<AKey, int>* table, bool* opened
   }
   for (const auto& c : rows) {
     try {
-      if (c.size() == 7 && c[0] == "F") {
-        const int mode = std::stoi(c[6]);
-        if (validSplit(mode)) {
-          (*table)[AKey{'F', std::stoull(c[1]), std::stoull(c[2]), std::stoi(c[3]), std::stoi(c[4]),
-                        std::stoi(c[5]), 0}] = mode;
-        }
-      } else if (c.size() == 8 && c[0] == "T") {
+      if (c.size() == 8 && c[0] == "HF") {
         const int mode = std::stoi(c[7]);
         if (validSplit(mode)) {
-          (*table)[AKey{'T', std::stoull(c[1]), std::stoull(c[2]), std::stoi(c[3]), std::stoi(c[4]),
-                        std::stoi(c[5]), std::stoi(c[6])}] = mode;
+          (*table)[AKey{'F', std::stoull(c[1]), std::stoull(c[2]), std::stoi(c[3]), std::stoi(c[4]),
+                        std::stoi(c[5]), 0, c[6]}] = mode;
         }
+      } else if (c.size() == 9 && c[0] == "HT") {
+        const int mode = std::stoi(c[8]);
+        if (validSplit(mode)) {
+          (*table)[AKey{'T', std::stoull(c[1]), std::stoull(c[2]), std::stoi(c[3]), std::stoi(c[4]),
+                        std::stoi(c[5]), std::stoi(c[6]), c[7]}] = mode;
+        }
+      } else if ((c.size() == 7 && c[0] == "F") || (c.size() == 8 && c[0] == "T")) {
+        foreign->push_back(joinCsv(c));
       }
     } catch (...) {
       // malformed rows are ignored
@@ -269,20 +285,23 @@ bool parseAttn(const std::string& path, std::map<AKey, int>* table, bool* opened
   return true;
 }
 
-bool writeAttn(const std::string& path, const std::map<AKey, int>& table) {
+bool writeAttn(const std::string& path, const std::map<AKey, int>& table, const std::vector<std::string>& foreign) {
   std::ofstream f(path, std::ios::trunc);
   if (!f.is_open()) {
     return false;
   }
-  f << kTag << ",attention," << kVersion << "\n" << kAttnColumns << "\n";
+  f << kTag << ",attention," << kVersion << "\n" << kAttnColumns << "\n" << kAttnHipColumns << "\n";
+  for (const auto& row : foreign) {
+    f << row << "\n";
+  }
   for (const auto& kv : table) {
     const auto& k = kv.first;
-    f << std::get<0>(k) << "," << std::get<1>(k) << "," << std::get<2>(k) << "," << std::get<3>(k) << ","
-      << std::get<4>(k) << "," << std::get<5>(k) << ",";
+    f << (std::get<0>(k) == 'T' ? "HT" : "HF") << "," << std::get<1>(k) << "," << std::get<2>(k) << ","
+      << std::get<3>(k) << "," << std::get<4>(k) << "," << std::get<5>(k) << ",";
     if (std::get<0>(k) == 'T') {
       f << std::get<6>(k) << ",";
     }
-    f << kv.second << "\n";
+    f << std::get<7>(k) << "," << kv.second << "\n";
   }
   return f.good();
 }
@@ -295,10 +314,12 @@ void loadAttnOnce(AttnCache& c) {
   c.path = pathFrom("CJ_ATTN_TUNE_CACHE_FILE", ".lightning_core_attn_tune_cache.csv");
   bool opened = false;
   std::map<AKey, int> t;
-  if (parseAttn(c.path, &t, &opened)) {
+  std::vector<std::string> foreign;
+  if (parseAttn(c.path, &t, &foreign, &opened)) {
     for (auto& kv : t) {
       c.table.insert(kv);
     }
+    c.foreign = std::move(foreign);
   }
 }
 
@@ -371,7 +392,7 @@ void attnTuneRecord(const AttnTuneKey& key, int mode) {
     return;
   }
   c.table[k] = mode;
-  (void)writeAttn(c.path, c.table);
+  (void)writeAttn(c.path, c.table, c.foreign);
 }
 
 void attnTuneReset() {
@@ -507,7 +528,7 @@ lcError_t lcHipAttentionTuneCacheSave(const char* path) {
   AttnCache& c = at();
   std::lock_guard<std::mutex> lock(c.mu);
   loadAttnOnce(c);
-  if (!writeAttn(path, c.table)) {
+  if (!writeAttn(path, c.table, c.foreign)) {
     return toLc(fail(Status::kInvalidValue, std::string("attention tune cache: cannot write ") + path));
   }
   return LC_SUCCESS;
@@ -518,8 +539,9 @@ lcError_t lcHipAttentionTuneCacheLoad(const char* path) {
     return LC_INVALID_VALUE;
   }
   std::map<AKey, int> t;
+  std::vector<std::string> foreign;
   bool opened = false;
-  const bool ok = parseAttn(path, &t, &opened);
+  const bool ok = parseAttn(path, &t, &foreign, &opened);
   AttnCache& c = at();
   std::lock_guard<std::mutex> lock(c.mu);
   if (!opened) {
@@ -529,9 +551,11 @@ lcError_t lcHipAttentionTuneCacheLoad(const char* path) {
   c.path = path;
   if (!ok) {
     c.table.clear();
+    c.foreign.clear();
     return toLc(fail(Status::kInvalidValue, "attention tune cache: unsupported header (cache cleared)"));
   }
   c.table = std::move(t);
+  c.foreign = std::move(foreign);
   return LC_SUCCESS;
 }
 

@@ -28,10 +28,12 @@ bool tuneLookup(std::size_t m, std::size_t k, std::size_t n, int dtype, const st
 void tuneReset();
 std::size_t tuneSize();
 
-// The attention cache, in the reference's row layout: kind 'F' (forward) or
-// 'T' (train step), seq, dim, causal, resident_hint, sync_hint, [compute_loss
-// for 'T'], mode.  On gfx950 the mode is the fp32 kernel's split count
-// (1, 2, 4 or 8 waves per 32 queries; the train step's dV kernel for 'T').
+// The attention cache: the reference's key (kind 'F' forward or 'T' train
+// step, seq, dim, causal, resident_hint, sync_hint, compute_loss for 'T')
+// plus the arch; the value is the fp32 kernel's split count (1, 2, 4 or 8
+// waves per 32 queries; the train step's dV kernel for 'T').  The file
+// holds them as HF / HT rows next to the reference's own F / T rows, which are
+// kept but never read as split counts.
 // File: CJ_ATTN_TUNE_CACHE_FILE, else .lightning_core_attn_tune_cache.csv.
 struct AttnTuneKey {
   char kind = 'F';
@@ -41,6 +43,7 @@ struct AttnTuneKey {
   uint8_t resident_hint = 0;
   uint8_t sync_hint = 0;
   uint8_t compute_loss = 0;  // 'T' rows only
+  std::string arch;          // e.g. "gfx950"
 };
 bool attnTuneLookup(const AttnTuneKey& key, int* mode);
 void attnTuneRecord(const AttnTuneKey& key, int mode);

@@ -2,6 +2,7 @@
 from __future__ import annotations
 
 import ctypes
+import threading
 
 import numpy as np
 
@@ -14,9 +15,14 @@ __all__ = [
     "clear_attention2d_session_cache", "attention_batched", "attention_implementation_name",
     "matmul2d", "matmul2d_into", "matmul", "matmul_np", "matmul_np_into", "matmul_with_policy",
     "matmul2d_resident_session", "matmul_reset_tuning", "conv2d_nchw", "vit_block",
-    "runtime_backend_capabilities", "runtime_backend_interface_contract", "backend_name", "is_hip_available",
-    "is_cuda_available", "is_metal_available", "device_info", "api_version", "runtime_trace_enable",
-    "runtime_trace_clear", "runtime_trace_events", "runtime_trace_event_capacity", "decode_dispatch_detail",
+    "matmul_np_with_policy", "matmul_np_into_with_policy", "conv2d_nchw_into",
+    "runtime_backend_capabilities", "runtime_active_backend_capabilities", "runtime_backend_interfaces",
+    "runtime_active_backend_interfaces", "runtime_backend_interface_contract", "backend_name", "is_hip_available",
+    "hip_available", "cuda_available", "metal_available", "is_cuda_available", "is_metal_available",
+    "memory_model_name", "runtime_sync_policy_set", "runtime_sync_policy_get", "runtime_sync_apply",
+    "runtime_sync_apply_default", "device_info", "api_version", "runtime_trace_enable", "runtime_trace_enabled",
+    "runtime_trace_clear", "runtime_trace_events", "runtime_trace_capacity", "runtime_trace_event_capacity",
+    "runtime_trace_timeline", "decode_dispatch_detail",
     "tune_cache_save", "tune_cache_load", "tune_cache_size", "attention_tune_cache_save",
     "attention_tune_cache_load", "attention_reset_tuning", "attention_tune_cache_size",
     "preload_runtime_profile_env", "device_synchronize", "LightningCoreError",
@@ -34,6 +40,10 @@ class LightningCoreError(RuntimeError):
     def __init__(self, status: int, message: str):
         super().__init__(message)
         self.status = status
+
+
+class SessionClosedError(LightningCoreError):
+    """A call on a session that close() (or the session-cache clear) ended."""
 
 
 def _lib():
@@ -164,6 +174,11 @@ class AttentionSession:
                                                        ctypes.byref(h)))
             self.shape = (_batched.batch, _batched.heads, _batched.seq_len, _batched.head_dim)
         self._h = h
+        # Held around every C call on the handle and around close(): ctypes
+        # drops the GIL during a call, so without it another thread could
+        # destroy the session while a call still uses it.  The library's
+        # context mutex serialises the device work itself.
+        self._lock = threading.RLock()
         self.causal = bool(causal)
         self.device = device
 
@@ -172,10 +187,20 @@ class AttentionSession:
         cfg = N.AttentionBatchedConfig(batch, heads, seq_len, head_dim, int(causal), _parse_dtype(compute_dtype))
         return cls(seq_len, head_dim, causal, device, _batched=cfg)
 
+    def _invoke(self, fname, *args):
+        with self._lock:
+            if not self._h.value:
+                raise SessionClosedError(N.LC_INVALID_VALUE, "attention session is closed")
+            return getattr(_lib(), fname)(self._h, *args)
+
     def close(self):
-        if getattr(self, "_h", None) and self._h.value:
-            _lib().lcAttentionSessionDestroy(self._h)
-            self._h = ctypes.c_void_p()
+        lock = getattr(self, "_lock", None)
+        if lock is None:
+            return
+        with lock:
+            if self._h.value:
+                _lib().lcAttentionSessionDestroy(self._h)
+                self._h = ctypes.c_void_p()
 
     def __del__(self):
         try:
@@ -189,11 +214,11 @@ class AttentionSession:
 
     def set_default_policy(self, policy: AttentionIoPolicy):
         c = policy._c()
-        _check(_lib().lcAttentionSessionSetDefaultPolicy(self._h, ctypes.byref(c)))
+        _check(self._invoke("lcAttentionSessionSetDefaultPolicy", ctypes.byref(c)))
 
     def default_policy(self) -> AttentionIoPolicy:
         c = N.AttentionIoPolicyC()
-        _check(_lib().lcAttentionSessionGetDefaultPolicy(self._h, ctypes.byref(c)))
+        _check(self._invoke("lcAttentionSessionGetDefaultPolicy", ctypes.byref(c)))
         return AttentionIoPolicy._from_c(c)
 
     def _args(self, q, k, v):
@@ -205,32 +230,32 @@ class AttentionSession:
     def forward(self, q, k, v):
         q, k, v = self._args(q, k, v)
         out = np.zeros(self.numel, np.float32)
-        _check(_lib().lcAttentionSessionForward(self._h, _fp(q), _fp(k), _fp(v), _fp(out)))
+        _check(self._invoke("lcAttentionSessionForward", _fp(q), _fp(k), _fp(v), _fp(out)))
         return out
 
     def forward_with_policy(self, q, k, v, policy: AttentionIoPolicy):
         q, k, v = self._args(q, k, v)
         out = np.zeros(self.numel, np.float32)
         c = policy._c()
-        _check(_lib().lcAttentionSessionForwardWithPolicy(self._h, _fp(q), _fp(k), _fp(v), _fp(out),
-                                                          ctypes.byref(c)))
+        _check(self._invoke("lcAttentionSessionForwardWithPolicy", _fp(q), _fp(k), _fp(v), _fp(out),
+                            ctypes.byref(c)))
         return out
 
     def forward_into(self, q, k, v, out):
         q, k, v = self._args(q, k, v)
         _require_out(out, self.numel)
-        _check(_lib().lcAttentionSessionForward(self._h, _fp(q), _fp(k), _fp(v), _fp(out)))
+        _check(self._invoke("lcAttentionSessionForward", _fp(q), _fp(k), _fp(v), _fp(out)))
 
     def forward_with_policy_into(self, q, k, v, out, policy: AttentionIoPolicy):
         q, k, v = self._args(q, k, v)
         _require_out(out, self.numel)
         c = policy._c()
-        _check(_lib().lcAttentionSessionForwardWithPolicy(self._h, _fp(q), _fp(k), _fp(v), _fp(out),
-                                                          ctypes.byref(c)))
+        _check(self._invoke("lcAttentionSessionForwardWithPolicy", _fp(q), _fp(k), _fp(v), _fp(out),
+                            ctypes.byref(c)))
 
     def run_cached(self, repeat_count: int = 1):
         """Launch-only repeat over the resident inputs, then synchronise."""
-        _check(_lib().lcAttentionSessionRunCached(self._h, repeat_count))
+        _check(self._invoke("lcAttentionSessionRunCached", repeat_count))
 
     def _train_args(self, q, k, v, target):
         q, k, v = self._args(q, k, v)
@@ -245,8 +270,8 @@ class AttentionSession:
         q, k, v, target = self._train_args(q, k, v, target)
         out = np.zeros(self.numel, np.float32)
         loss = ctypes.c_float(0.0)
-        _check(_lib().lcAttentionSessionTrainStep(self._h, _fp(q), _fp(k), _fp(v), _fp(target), _fp(out),
-                                                  float(learning_rate), ctypes.pointer(loss)))
+        _check(self._invoke("lcAttentionSessionTrainStep", _fp(q), _fp(k), _fp(v), _fp(target), _fp(out),
+                            float(learning_rate), ctypes.pointer(loss)))
         return out, v, float(loss.value)
 
     def train_step_with_policy(self, q, k, v, target, learning_rate: float, policy: AttentionIoPolicy):
@@ -255,9 +280,8 @@ class AttentionSession:
         out = np.zeros(self.numel, np.float32)
         loss = ctypes.c_float(0.0)
         c = policy._c()
-        _check(_lib().lcAttentionSessionTrainStepWithPolicy(self._h, _fp(q), _fp(k), _fp(v), _fp(target), _fp(out),
-                                                            float(learning_rate), ctypes.pointer(loss),
-                                                            ctypes.byref(c)))
+        _check(self._invoke("lcAttentionSessionTrainStepWithPolicy", _fp(q), _fp(k), _fp(v), _fp(target), _fp(out),
+                            float(learning_rate), ctypes.pointer(loss), ctypes.byref(c)))
         return out, v, float(loss.value)
 
 
@@ -269,28 +293,54 @@ def _require_out(out, n):
 
 
 _session_cache: dict = {}
+_session_cache_lock = threading.Lock()
+_session_tls = threading.local()
 
 
 def clear_attention2d_session_cache():
-    """bind_attention.cpp:124-127."""
-    for s in _session_cache.values():
+    """bind_attention.cpp:124-127.  Closes the cached sessions; a call already
+    running on one finishes first (the session's own lock)."""
+    with _session_cache_lock:
+        sessions = list(_session_cache.values())
+        _session_cache.clear()
+    for s in sessions:
         s.close()
-    _session_cache.clear()
 
 
 def _cached_session(seq_len, head_dim, causal, device):
-    """bind_attention.cpp:36-69: one session per (S, D, causal, device).
+    """bind_attention.cpp:36-69: one session per (S, D, causal, device), found
+    through a per-thread last-session slot, else the shared map under a lock.
 
     The cached session uses the reference's one-shot policy (upload, download,
     synchronize) so every call is self-contained.
     """
     key = (seq_len, head_dim, bool(causal), device)
-    s = _session_cache.get(key)
+    slot = getattr(_session_tls, "slot", None)
+    if slot is not None and slot[0] == key and slot[1]._h.value:
+        return slot[1]
+    with _session_cache_lock:
+        s = _session_cache.get(key)
     if s is None:
-        s = AttentionSession(seq_len, head_dim, causal, device)
-        s.set_default_policy(AttentionIoPolicy())
-        _session_cache[key] = s
+        fresh = AttentionSession(seq_len, head_dim, causal, device)
+        fresh.set_default_policy(AttentionIoPolicy())
+        with _session_cache_lock:
+            s = _session_cache.setdefault(key, fresh)
+        if s is not fresh:  # another thread inserted one first
+            fresh.close()
+    _session_tls.slot = (key, s)
     return s
+
+
+def _cached_forward_into(seq_len, head_dim, causal, device, q, k, v, out):
+    """Forward on the cached session; if a concurrent cache clear closed it
+    between lookup and call, the lookup runs once more (a new session)."""
+    for attempt in range(2):
+        try:
+            _cached_session(seq_len, head_dim, causal, device).forward_into(q, k, v, out)
+            return
+        except SessionClosedError:
+            if attempt:
+                raise
 
 
 def _attn2d_shapes(q, k, v):
@@ -307,7 +357,7 @@ def attention2d(q, k, v, causal: bool = False, device: str = "hip"):
     """bind_attention.cpp:298-327."""
     q, k, v, s, d = _attn2d_shapes(q, k, v)
     out = np.empty((s, d), np.float32)
-    _cached_session(s, d, causal, _check_dev(device)).forward_into(q, k, v, out)
+    _cached_forward_into(s, d, causal, _check_dev(device), q, k, v, out)
     return out
 
 
@@ -316,7 +366,7 @@ def attention2d_into(q, k, v, out, causal: bool = False, device: str = "hip"):
     q, k, v, s, d = _attn2d_shapes(q, k, v)
     if not isinstance(out, np.ndarray) or out.shape != (s, d):
         raise ValueError("out must be a 2D float32 array shaped [seq_len, head_dim]")
-    _cached_session(s, d, causal, _check_dev(device)).forward_into(q, k, v, out)
+    _cached_forward_into(s, d, causal, _check_dev(device), q, k, v, out)
 
 
 def attention_forward(q, k, v, seq_len: int, head_dim: int, causal: bool = False, device: str = "hip"):
@@ -327,7 +377,7 @@ def attention_forward(q, k, v, seq_len: int, head_dim: int, causal: bool = False
         if a.size != n:
             raise ValueError(f"{name} size mismatch")
     out = np.empty(n, np.float32)
-    _cached_session(seq_len, head_dim, causal, _check_dev(device)).forward_into(q, k, v, out)
+    _cached_forward_into(seq_len, head_dim, causal, _check_dev(device), q, k, v, out)
     return out
 
 
@@ -429,17 +479,52 @@ def matmul_np_into(a, b, out, m: int, k: int, n: int, device: str = "hip"):
     _mm_policy_call(a, b, out, m, k, n, device, MatMulIoPolicy())
 
 
-def matmul_with_policy(a, b, m: int, k: int, n: int, device: str = "hip", policy: MatMulIoPolicy | None = None,
-                       out=None):
-    """ops::matMulWithPolicy<float>: a/b may be None when not uploaded; returns
-    `out` (allocated when None and downloaded)."""
-    policy = policy or MatMulIoPolicy()
+def _policy_operands(a, b, m, k, n, policy):
+    """bind_ops.cpp:635-726: a and b must hold m*k and k*n floats.  Here an
+    operand may also be None: the C entry then uses the resident one when the
+    policy does not upload it, and answers "invalid value" when it does
+    (ops.hpp:367-370).  An operand that is given is checked all the same."""
     a = None if a is None else _f32(a).ravel()
     b = None if b is None else _f32(b).ravel()
-    if out is None and policy.download_out:
-        out = np.zeros(m * n, np.float32)
+    if (a is not None and a.size != m * k) or (b is not None and b.size != k * n):
+        raise ValueError("a or b shape mismatch")
+    return a, b
+
+
+def matmul_with_policy(a, b, m: int, k: int, n: int, device: str = "hip", policy: MatMulIoPolicy | None = None,
+                       out=None):
+    """bind_ops.cpp:635-675 (ops::matMulWithPolicy<float>): returns `out`
+    (allocated when None and the policy downloads; else checked: a C-contiguous
+    float32 array of m*n values)."""
+    policy = policy or MatMulIoPolicy()
+    a, b = _policy_operands(a, b, m, k, n, policy)
+    if out is None:
+        if policy.download_out:
+            out = np.zeros(m * n, np.float32)
+    else:
+        _require_out(out, m * n)
     _mm_policy_call(a, b, out, m, k, n, device, policy)
     return out
+
+
+def matmul_np_with_policy(a, b, m: int, k: int, n: int, device: str = "hip", policy: MatMulIoPolicy | None = None):
+    """bind_ops.cpp:677-699: flat float32 result of m*n values."""
+    policy = policy or MatMulIoPolicy()
+    a, b = _policy_operands(a, b, m, k, n, policy)
+    out = np.zeros(m * n, np.float32)
+    _mm_policy_call(a, b, out, m, k, n, device, policy)
+    return out
+
+
+def matmul_np_into_with_policy(a, b, out, m: int, k: int, n: int, device: str = "hip",
+                               policy: MatMulIoPolicy | None = None):
+    """bind_ops.cpp:701-726."""
+    policy = policy or MatMulIoPolicy()
+    a, b = _policy_operands(a, b, m, k, n, policy)
+    if not isinstance(out, np.ndarray) or out.size != m * n:
+        raise ValueError("out shape mismatch")
+    _require_out(out, m * n)
+    _mm_policy_call(a, b, out, m, k, n, device, policy)
 
 
 def matmul_reset_tuning():
@@ -544,12 +629,8 @@ def matmul2d_resident_session(a, b, compute_dtype: str = "f32"):
 
 # --- conv / vit -----------------------------------------------------------------
 
-def conv2d_nchw(x, w, bias=None, stride_h=1, stride_w=1, pad_h=0, pad_w=0, device: str = "hip",
-                apply_relu: bool = False):
-    """ops::conv2dNchw<float> (ops.hpp:855-1213): x [B,C,H,W], w [OC,C,KH,KW]."""
-    x, w = _f32(x), _f32(w)
-    if x.ndim != 4 or w.ndim != 4:
-        raise ValueError("x and w must be 4D arrays (NCHW and OIHW)")
+def _conv_geometry(x, w, stride_h, stride_w, pad_h, pad_w):
+    """bind_ops.cpp:737-765 / :818-846: validation and output size."""
     bn, c, h, wd = x.shape
     oc, wc, kh, kw = w.shape
     if c != wc:
@@ -560,15 +641,51 @@ def conv2d_nchw(x, w, bias=None, stride_h=1, stride_w=1, pad_h=0, pad_w=0, devic
         raise ValueError("invalid padding/kernel for input size")
     oh = (h + 2 * pad_h - kh) // stride_h + 1
     ow = (wd + 2 * pad_w - kw) // stride_w + 1
-    b = None
-    if bias is not None:
-        b = _f32(bias).ravel()
-        if b.size != oc:
-            raise ValueError("bias shape mismatch")
-    out = np.empty((bn, oc, oh, ow), np.float32)
+    return (bn, c, h, wd, oc, kh, kw), (bn, oc, oh, ow)
+
+
+def _conv_bias(bias, oc):
+    if bias is None:
+        return None
+    b = _f32(bias).ravel()
+    if b.size != oc:
+        raise ValueError("bias shape mismatch")
+    return b
+
+
+def _conv_call(x, w, b, out, dims, stride_h, stride_w, pad_h, pad_w, device, apply_relu):
+    bn, c, h, wd, oc, kh, kw = dims
     _check(_lib().lcConv2dNchw(_fp(x), _fp(w), _fp(b), _fp(out), bn, c, h, wd, oc, kh, kw, stride_h, stride_w, pad_h,
                                pad_w, _parse_device(device), int(apply_relu)))
+
+
+def conv2d_nchw(x, w, bias=None, stride_h=1, stride_w=1, pad_h=0, pad_w=0, device: str = "hip",
+                apply_relu: bool = False):
+    """ops::conv2dNchw<float> (ops.hpp:855-1213), bind_ops.cpp:728-804:
+    x [B,C,H,W], w [OC,C,KH,KW] -> [B,OC,OH,OW].  `apply_relu` is the
+    C++ entry's flag (default off, as there)."""
+    x, w = _f32(x), _f32(w)
+    if x.ndim != 4 or w.ndim != 4:
+        raise ValueError("x and w must be 4D arrays (NCHW and OIHW)")
+    dims, oshape = _conv_geometry(x, w, stride_h, stride_w, pad_h, pad_w)
+    b = _conv_bias(bias, dims[4])
+    out = np.empty(oshape, np.float32)
+    _conv_call(x, w, b, out, dims, stride_h, stride_w, pad_h, pad_w, device, apply_relu)
     return out
+
+
+def conv2d_nchw_into(x, w, bias, out, stride_h=1, stride_w=1, pad_h=0, pad_w=0, device: str = "hip",
+                     apply_relu: bool = False):
+    """bind_ops.cpp:806-888: writes into a 4-D float32 `out` of the output shape."""
+    x, w = _f32(x), _f32(w)
+    if x.ndim != 4 or w.ndim != 4 or not isinstance(out, np.ndarray) or out.ndim != 4:
+        raise ValueError("x, w, out must be 4D arrays")
+    dims, oshape = _conv_geometry(x, w, stride_h, stride_w, pad_h, pad_w)
+    if tuple(out.shape) != oshape:
+        raise ValueError("out shape mismatch")
+    _require_out(out, out.size)
+    b = _conv_bias(bias, dims[4])
+    _conv_call(x, w, b, out, dims, stride_h, stride_w, pad_h, pad_w, device, apply_relu)
 
 
 class VitBlockSession:
@@ -643,25 +760,58 @@ def _caps_dict(c) -> dict:
 
 
 def runtime_backend_capabilities(device: str = "hip") -> dict:
-    """bind_runtime.cpp:421-435."""
+    """bind_runtime.cpp:421-425."""
     c = N.BackendCapabilities()
     _check(_lib().lcGetBackendCapabilities(_parse_device(device), ctypes.byref(c)))
     return _caps_dict(c)
 
 
-def runtime_backend_interface_contract(device: str = "hip") -> dict:
+def runtime_active_backend_capabilities() -> dict:
+    """bind_runtime.cpp:426-427."""
+    c = N.BackendCapabilities()
+    _check(_lib().lcGetActiveBackendCapabilities(ctypes.byref(c)))
+    return _caps_dict(c)
+
+
+def _contract_dict(c) -> dict:
+    """bind_runtime.cpp:39-77 (toBackendInterfaceContractDict)."""
+    model = _lib().lcGetMemoryModelName
+    return {"device": _DEVICE_NAMES.get(c.device, str(c.device)), "capabilities": _caps_dict(c.capabilities),
+            "compute": {"available": bool(c.compute.available),
+                        "op_dispatch_trace_surface": bool(c.compute.op_dispatch_trace_surface),
+                        "driver_tag": c.compute.driver_tag.decode()},
+            "memory": {"available": bool(c.memory.available), "allocator_surface": bool(c.memory.allocator_surface),
+                       "memcpy_surface": bool(c.memory.memcpy_surface),
+                       "memory_model": model(c.memory.memory_model).decode(),
+                       "driver_tag": c.memory.driver_tag.decode()},
+            "sync": {"available": bool(c.sync.available), "sync_policy_surface": bool(c.sync.sync_policy_surface),
+                     "trace_sync_boundary_surface": bool(c.sync.trace_sync_boundary_surface),
+                     "driver_tag": c.sync.driver_tag.decode()},
+            "profiler": {"available": bool(c.profiler.available),
+                         "runtime_trace_surface": bool(c.profiler.runtime_trace_surface),
+                         "op_dispatch_trace_surface": bool(c.profiler.op_dispatch_trace_surface),
+                         "trace_capacity": c.profiler.trace_capacity, "driver_tag": c.profiler.driver_tag.decode()}}
+
+
+def runtime_backend_interfaces(device: str = "hip") -> dict:
+    """bind_runtime.cpp:428-432."""
     c = N.BackendInterfaceContract()
     _check(_lib().lcGetBackendInterfaceContract(_parse_device(device), ctypes.byref(c)))
-    return {"device": _DEVICE_NAMES.get(c.device), "capabilities": _caps_dict(c.capabilities),
-            "compute": {"available": bool(c.compute.available), "driver_tag": c.compute.driver_tag.decode()},
-            "memory": {"available": bool(c.memory.available), "allocator_surface": bool(c.memory.allocator_surface),
-                       "driver_tag": c.memory.driver_tag.decode()},
-            "sync": {"available": bool(c.sync.available), "driver_tag": c.sync.driver_tag.decode()},
-            "profiler": {"available": bool(c.profiler.available), "trace_capacity": c.profiler.trace_capacity,
-                         "driver_tag": c.profiler.driver_tag.decode()}}
+    return _contract_dict(c)
+
+
+def runtime_active_backend_interfaces() -> dict:
+    """bind_runtime.cpp:433-434."""
+    c = N.BackendInterfaceContract()
+    _check(_lib().lcGetActiveBackendInterfaceContract(ctypes.byref(c)))
+    return _contract_dict(c)
+
+
+runtime_backend_interface_contract = runtime_backend_interfaces
 
 
 def backend_name() -> str:
+    """bind_runtime.cpp:392."""
     return _lib().lcBackendName().decode()
 
 
@@ -669,12 +819,57 @@ def is_hip_available() -> bool:
     return bool(_lib().lcIsHipAvailable())
 
 
-def is_cuda_available() -> bool:
+def cuda_available() -> bool:
+    """bind_runtime.cpp:390."""
     return bool(_lib().lcIsCudaAvailable())
 
 
-def is_metal_available() -> bool:
+def metal_available() -> bool:
+    """bind_runtime.cpp:391."""
     return bool(_lib().lcIsMetalAvailable())
+
+
+hip_available = is_hip_available
+is_cuda_available = cuda_available
+is_metal_available = metal_available
+
+
+def memory_model_name() -> str:
+    """bind_runtime.cpp:393-394."""
+    lib = _lib()
+    return lib.lcGetMemoryModelName(lib.lcGetMemoryModel()).decode()
+
+
+_SYNC_MODES = {"auto": 0, "always": 1, "never": 2}
+_SYNC_MODE_NAMES = {v: k for k, v in _SYNC_MODES.items()}
+
+
+def _sync_policy(mode, trace_sync_boundary):
+    """bind_runtime.cpp:11-22 (parseSyncMode)."""
+    if mode not in _SYNC_MODES:
+        raise ValueError("sync mode must be 'auto', 'always', or 'never'")
+    return N.SyncPolicy(_SYNC_MODES[mode], int(bool(trace_sync_boundary)))
+
+
+def runtime_sync_policy_set(mode: str = "auto", trace_sync_boundary: bool = False):
+    """bind_runtime.cpp:395-403."""
+    _check(_lib().lcSetDefaultSyncPolicy(_sync_policy(mode, trace_sync_boundary)))
+
+
+def runtime_sync_policy_get() -> dict:
+    """bind_runtime.cpp:404-410."""
+    p = _lib().lcGetDefaultSyncPolicy()
+    return {"mode": _SYNC_MODE_NAMES.get(p.mode, "auto"), "trace_sync_boundary": bool(p.trace_sync_boundary)}
+
+
+def runtime_sync_apply(mode: str = "auto", trace_sync_boundary: bool = False):
+    """bind_runtime.cpp:411-419 (deviceSynchronizeWithPolicy)."""
+    _check(_lib().lcApplySyncPolicy(_sync_policy(mode, trace_sync_boundary)))
+
+
+def runtime_sync_apply_default():
+    """bind_runtime.cpp:420."""
+    _check(_lib().lcApplyDefaultSyncPolicy())
 
 
 def device_synchronize():
@@ -696,15 +891,26 @@ def api_version():
 
 
 def runtime_trace_enable(enabled: bool = True):
+    """bind_runtime.cpp:435."""
     _lib().lcSetRuntimeTraceEnabled(int(enabled))
 
 
+def runtime_trace_enabled() -> bool:
+    """bind_runtime.cpp:436."""
+    return bool(_lib().lcIsRuntimeTraceEnabled())
+
+
 def runtime_trace_clear():
+    """bind_runtime.cpp:437."""
     _lib().lcClearRuntimeTraceEvents()
 
 
-def runtime_trace_event_capacity() -> int:
+def runtime_trace_capacity() -> int:
+    """bind_runtime.cpp:438."""
     return int(_lib().lcGetRuntimeTraceEventCapacity())
+
+
+runtime_trace_event_capacity = runtime_trace_capacity
 
 
 def decode_dispatch_detail(encoded: int):
@@ -714,22 +920,143 @@ def decode_dispatch_detail(encoded: int):
     return {"requested": _DEVICE_NAMES[r.value], "selected": _DEVICE_NAMES[s.value], "fallback": bool(f.value)}
 
 
-def runtime_trace_events() -> list:
-    """bind_runtime.cpp:439-470: events as dicts, oldest first."""
+def _raw_trace_events():
     lib = _lib()
     n = lib.lcGetRuntimeTraceEvents(None, 0)
     arr = (N.RuntimeTraceEvent * max(n, 1))()
     got = lib.lcGetRuntimeTraceEvents(arr, n)
-    out = []
-    for ev in arr[:got]:
-        d = {"type": lib.lcRuntimeTraceEventTypeName(ev.type).decode(), "status": ev.status,
-             "timestamp_ns": ev.timestamp_ns, "size_bytes": ev.size_bytes, "detail0": ev.detail0,
-             "detail1": ev.detail1}
-        if d["type"] == "op_dispatch":
-            d["op"] = lib.lcRuntimeTraceOpKindName(ev.detail0).decode()
-            d.update(decode_dispatch_detail(ev.detail1) or {})
-        out.append(d)
+    return lib, arr[:got]
+
+
+def _trace_row(lib, ev) -> dict:
+    """One event with its op-dispatch fields decoded (bind_runtime.cpp:117-141,
+    :439-464); op and devices are "" for other event types."""
+    row = {"type": lib.lcRuntimeTraceEventTypeName(ev.type).decode(),
+           "status": lib.lcGetErrorString(ev.status).decode(), "timestamp_ns": int(ev.timestamp_ns),
+           "size_bytes": int(ev.size_bytes), "detail0": int(ev.detail0), "detail1": int(ev.detail1),
+           "op": "", "requested_device": "", "selected_device": "", "fallback": False}
+    if row["type"] == "op_dispatch":
+        row["op"] = lib.lcRuntimeTraceOpKindName(ev.detail0).decode()
+        d = decode_dispatch_detail(ev.detail1)
+        if d is not None:
+            row["requested_device"] = d["requested"]
+            row["selected_device"] = d["selected"]
+            row["fallback"] = d["fallback"]
+    return row
+
+
+def runtime_trace_events() -> list:
+    """bind_runtime.cpp:439-464: events as dicts, oldest first."""
+    lib, events = _raw_trace_events()
+    return [_trace_row(lib, ev) for ev in events]
+
+
+_EVENT_SORT_KEYS = ("index", "timestamp_ns", "offset_ns", "delta_prev_ns", "delta_next_ns", "size_bytes")
+_GROUP_SORT_KEYS = ("key", "count", "total_delta_next_ns", "avg_delta_next_ns", "max_delta_next_ns",
+                    "total_size_bytes")
+
+
+def _timeline_group_key(row, group_by):
+    """bind_runtime.cpp:180-206 (makeGroupKey)."""
+    if group_by == "type":
+        return row["type"]
+    if group_by == "status":
+        return row["status"]
+    if group_by == "type_status":
+        return row["type"] + "|" + row["status"]
+    if group_by in ("op", "op_selected_device", "op_path"):
+        if not row["op"]:
+            return "non_op"
+        if group_by == "op":
+            return row["op"]
+        sel = row["selected_device"] or "unknown"
+        if group_by == "op_selected_device":
+            return row["op"] + "|" + sel
+        return row["op"] + "|" + sel + "|" + ("fallback" if row["fallback"] else "direct")
+    raise ValueError("group_by must be one of: type, status, type_status, op, op_selected_device, op_path")
+
+
+def _sorted_stable(rows, value, tie, descending):
+    """std::stable_sort with orderedLess on (value, then tie): descending
+    reverses both comparisons, as the reference's comparator does."""
+    return sorted(rows, key=lambda r: (value(r), tie(r)), reverse=descending)
+
+
+def runtime_trace_timeline(event_sort_by: str = "timestamp_ns", event_descending: bool = False,
+                           group_by: str = "type", group_sort_by: str = "total_delta_next_ns",
+                           group_descending: bool = True, hotspot_top_k: int = 8) -> dict:
+    """bind_runtime.cpp:465-529: the trace as a timeline (offsets and gaps
+    between consecutive events), grouped, with the largest gaps as hotspots."""
+    if event_sort_by not in _EVENT_SORT_KEYS:
+        raise ValueError("event_sort_by must be one of: " + ", ".join(_EVENT_SORT_KEYS))
+    if group_sort_by not in _GROUP_SORT_KEYS:
+        raise ValueError("group_sort_by must be one of: " + ", ".join(_GROUP_SORT_KEYS))
+    lib, events = _raw_trace_events()
+    rows = []
+    base = events[0].timestamp_ns if events else 0
+    for i, ev in enumerate(events):
+        row = _trace_row(lib, ev)
+        ts = row["timestamp_ns"]
+        prev_ts = events[i - 1].timestamp_ns if i > 0 else None
+        next_ts = events[i + 1].timestamp_ns if i + 1 < len(events) else None
+        row["index"] = i
+        row["offset_ns"] = ts - base if ts >= base else 0
+        row["delta_prev_ns"] = ts - prev_ts if prev_ts is not None and ts >= prev_ts else 0
+        row["delta_next_ns"] = next_ts - ts if next_ts is not None and next_ts >= ts else 0
+        rows.append(row)
+    out = {"event_count": len(rows), "event_sort_by": event_sort_by, "event_descending": bool(event_descending),
+           "group_by": group_by, "group_sort_by": group_sort_by, "group_descending": bool(group_descending),
+           "hotspot_top_k": int(hotspot_top_k),
+           "notes": "delta_next_ns is elapsed time until the next runtime trace event."}
+    if not rows:
+        out.update({"window_ns": 0, "events": [], "groups": [], "hotspots": []})
+        return out
+    window = rows[-1]["timestamp_ns"] - rows[0]["timestamp_ns"]
+    window = window if window >= 0 else 0
+    out["window_ns"] = window
+    out["events"] = [_timeline_event(r) for r in
+                     _sorted_stable(rows, lambda r: r[event_sort_by], lambda r: r["index"], event_descending)]
+    groups = {}
+    for r in rows:
+        key = _timeline_group_key(r, group_by)
+        g = groups.get(key)
+        if g is None:
+            g = groups[key] = {"key": key, "count": 0, "total_delta_next_ns": 0, "max_delta_next_ns": 0,
+                               "total_size_bytes": 0, "first_timestamp_ns": r["timestamp_ns"],
+                               "last_timestamp_ns": r["timestamp_ns"]}
+        g["last_timestamp_ns"] = r["timestamp_ns"]
+        g["count"] += 1
+        g["total_delta_next_ns"] += r["delta_next_ns"]
+        g["max_delta_next_ns"] = max(g["max_delta_next_ns"], r["delta_next_ns"])
+        g["total_size_bytes"] += r["size_bytes"]
+
+    def gvalue(g):
+        if group_sort_by == "avg_delta_next_ns":
+            return g["total_delta_next_ns"] // g["count"] if g["count"] else 0
+        return g[group_sort_by]
+
+    glist = list(groups.values())
+    if group_sort_by == "key":
+        glist = sorted(glist, key=lambda g: g["key"], reverse=group_descending)
+    else:
+        glist = _sorted_stable(glist, gvalue, lambda g: g["key"], group_descending)
+    for g in glist:
+        g["avg_delta_next_ns"] = g["total_delta_next_ns"] / g["count"] if g["count"] else 0.0
+        g["window_share_pct"] = 100.0 * g["total_delta_next_ns"] / window if window else 0.0
+    out["groups"] = [{k: g[k] for k in ("key", "count", "total_delta_next_ns", "avg_delta_next_ns",
+                                        "max_delta_next_ns", "total_size_bytes", "first_timestamp_ns",
+                                        "last_timestamp_ns", "window_share_pct")} for g in glist]
+    hot = _sorted_stable(rows, lambda r: r["delta_next_ns"], lambda r: r["index"], True)
+    limit = len(hot) if hotspot_top_k == 0 else min(int(hotspot_top_k), len(hot))
+    out["hotspots"] = [_timeline_event(r) for r in hot[:limit]]
     return out
+
+
+def _timeline_event(r) -> dict:
+    """bind_runtime.cpp:166-178 (toTimelineEventDict)."""
+    return {k: r[k] for k in ("index", "type", "status", "op", "requested_device", "selected_device", "fallback",
+                              "timestamp_ns", "offset_ns", "delta_prev_ns", "delta_next_ns", "size_bytes",
+                              "detail0", "detail1")}
 
 
 def tune_cache_save(path: str):

@@ -123,5 +123,5 @@ def test_attention_trace(lc):
     finally:
         lc.runtime_trace_enable(False)
     ev = [e for e in lc.runtime_trace_events() if e["type"] == "op_dispatch"]
-    assert ev[-1]["op"] == "attention_forward" and ev[-1]["selected"] == "hip"
+    assert ev[-1]["op"] == "attention_forward" and ev[-1]["selected_device"] == "hip"
     assert ev[-1]["size_bytes"] == 4 * 4 * 8

@@ -162,7 +162,7 @@ def test_trace_records_hip_dispatch(lc):
         lc.runtime_trace_enable(False)
     ev = [e for e in lc.runtime_trace_events() if e["type"] == "op_dispatch"]
     assert ev and ev[-1]["op"] == "matmul"
-    assert ev[-1]["requested"] == "hip" and ev[-1]["selected"] == "hip" and not ev[-1]["fallback"]
+    assert ev[-1]["requested_device"] == "hip" and ev[-1]["selected_device"] == "hip" and not ev[-1]["fallback"]
     assert ev[-1]["size_bytes"] == 4 * 7 * 5
 
 

@@ -80,8 +80,8 @@ def test_v1_seeded_caches_rewritten_after_autotune(lc, tmp_path):
     assert at[0] == "#lc_tune_cache,attention,2" and at[1].startswith("#columns,")
     assert "64,64,64,16,1,0" in mm  # the reference-layout row is kept
     assert any(r.startswith("16,16,16,0,gfx950,f32_") for r in mm)
-    assert any(r.startswith("F,16,16,0,") for r in at)
-    assert any(r.startswith("T,256,64,1,") for r in at)
+    assert any(r.startswith("HF,16,16,0,") and ",gfx950," in r for r in at)
+    assert any(r.startswith("HT,256,64,1,") and ",gfx950," in r for r in at)
 
 
 F32_CASES = [("f32_dp_64x64x64", (100, 130, 77)), ("f32_streamk_64x64x64", (257, 300, 64)),
@@ -188,8 +188,8 @@ def test_forced_attention_splits(lc, oracle, tmp_path, s, d, causal):
     caches = []
     for ks in (1, 2, 4, 8):
         cache = tmp_path / f"attn_{ks}.csv"
-        cache.write_text("#lc_tune_cache,attention,2\n" + f"F,{s},{d},{int(causal)},0,0,{ks}\n"
-                         + f"F,{s},{d},{int(causal)},0,1,{ks}\n")
+        cache.write_text("#lc_tune_cache,attention,2\n" + f"HF,{s},{d},{int(causal)},0,0,gfx950,{ks}\n"
+                         + f"HF,{s},{d},{int(causal)},0,1,gfx950,{ks}\n")
         caches.append((ks, str(cache)))
     out = _child(f"""
         import json

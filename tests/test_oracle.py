@@ -139,6 +139,52 @@ def test_attention_invariants(oracle):
     np.testing.assert_allclose(out, np.tile(v.mean(axis=0), (s, 1)), rtol=1e-4, atol=1e-5)
 
 
+def _batched_with_head_stride(oracle, q, k, v, causal, stride):
+    """The batched loop rebuilt from the per-head C function with an explicit
+    head stride (floats): the correct stride is S*D; other strides plant an
+    indexing mistake for the sensitivity check below."""
+    import ctypes
+
+    b, h, s, d = q.shape
+    q, k, v = (np.ascontiguousarray(x, np.float32) for x in (q, k, v))
+    out = np.zeros_like(q)
+    base = [x.ctypes.data for x in (q, k, v, out)]
+    for bh in range(b * h):
+        off = 4 * bh * stride
+        st = oracle.lib.orc_attention_forward(*(ctypes.c_void_p(p + off) for p in base), s, d, int(causal))
+        assert st == 0
+    return out
+
+
+@pytest.mark.parametrize("shape,causal", [((2, 3, 19, 8), False), ((2, 3, 19, 8), True), ((1, 4, 40, 24), True),
+                                          ((3, 1, 1, 5), False)])
+def test_attention_batched_pinned(oracle, shape, causal):
+    """orc_attention_forward_batched (the checker of every batched GPU case):
+    bit-equal to the per-head function on each [S, D] slice, and within 1e-5
+    of float64 brute force per head."""
+    q, k, v = (synth.normal(shape, seed=41, stream=i) for i in range(3))
+    got = oracle.attention_batched(q, k, v, causal)
+    b, h, s, d = shape
+    for bi in range(b):
+        for hi in range(h):
+            np.testing.assert_array_equal(got[bi, hi], oracle.attention(q[bi, hi], k[bi, hi], v[bi, hi], causal))
+            ref = _bf_attention(q[bi, hi], k[bi, hi], v[bi, hi], causal)
+            assert oracle_lib.normwise_rel(ref, got[bi, hi]) < 1e-5
+    np.testing.assert_array_equal(got, _batched_with_head_stride(oracle, q, k, v, causal, s * d))
+
+
+def test_attention_batched_catches_stride_mistake(oracle):
+    """A head offset of bh*S instead of bh*S*D (a dropped factor) fails the
+    per-head brute-force check the batched pin uses."""
+    shape = (2, 3, 16, 8)
+    q, k, v = (synth.normal(shape, seed=42, stream=i) for i in range(3))
+    s, d = shape[2], shape[3]
+    wrong = _batched_with_head_stride(oracle, q, k, v, True, s)
+    errs = [oracle_lib.normwise_rel(_bf_attention(q[bi, hi], k[bi, hi], v[bi, hi], True), wrong[bi, hi])
+            for bi in range(2) for hi in range(3)]
+    assert max(errs) > 1e-2
+
+
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (33, 64, 17)])
 def test_matmul_bruteforce(oracle, m, k, n):
     a, b = synth.uniform((m, k), seed=4, stream=1), synth.uniform((k, n), seed=4, stream=2)

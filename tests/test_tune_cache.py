@@ -117,11 +117,12 @@ def test_attention_cache_seed_and_rows(tmp_path):
     rows.write_text("\n".join([
         "#lc_tune_cache,attention,2",
         "#columns,kind,seq,dim,causal,resident_hint,sync_hint,compute_loss_or_mode,mode",
-        "F,256,64,0,1,0,4",
-        "F,2048,128,1,0,1,2",
-        "T,256,64,1,0,1,1,8",
-        "F,96,48,0,0,0,3",    # not a gfx950 split count: dropped
-        "T,96,48,0,0,0,1",    # T row without compute_loss: ignored
+        "HF,256,64,0,1,0,gfx950,4",
+        "HF,2048,128,1,0,1,gfx950,2",
+        "HT,256,64,1,0,1,1,gfx950,8",
+        "HF,256,64,0,1,0,gfx942,2",  # another arch: its own row, not this device's
+        "HF,96,48,0,0,0,gfx950,3",   # not a gfx950 split count: dropped
+        "HT,96,48,0,0,0,gfx950,1",   # HT row without compute_loss: ignored
     ]) + "\n", encoding="utf-8")
     out1 = tmp_path / "attn_out1.csv"
     out2 = tmp_path / "attn_out2.csv"
@@ -131,15 +132,44 @@ def test_attention_cache_seed_and_rows(tmp_path):
         assert lc.attention_tune_cache_size() == 0
         lc.attention_tune_cache_save({str(out1)!r})
         lc.attention_tune_cache_load({str(rows)!r})
-        assert lc.attention_tune_cache_size() == 3, lc.attention_tune_cache_size()
+        assert lc.attention_tune_cache_size() == 4, lc.attention_tune_cache_size()
         lc.attention_tune_cache_save({str(out2)!r})
         lc.attention_reset_tuning()
         assert lc.attention_tune_cache_size() == 0
     """, tmp_path)
     l1 = _lines(out1)
-    assert l1 == ["#lc_tune_cache,attention,2",
-                  "#columns,kind,seq,dim,causal,resident_hint,sync_hint,compute_loss_or_mode,mode"]
-    assert sorted(_lines(out2)[2:]) == sorted(["F,256,64,0,1,0,4", "F,2048,128,1,0,1,2", "T,256,64,1,0,1,1,8"])
+    assert l1[0] == "#lc_tune_cache,attention,2"
+    assert l1[1] == "#columns,kind,seq,dim,causal,resident_hint,sync_hint,compute_loss_or_mode,mode"
+    assert l1[2].startswith("#columns_hip,") and len(l1) == 3
+    assert sorted(_lines(out2)[3:]) == sorted(["HF,256,64,0,1,0,gfx950,4", "HF,2048,128,1,0,1,gfx950,2",
+                                               "HT,256,64,1,0,1,1,gfx950,8", "HF,256,64,0,1,0,gfx942,2"])
+
+
+def test_attention_cache_keeps_reference_rows(tmp_path):
+    """A file the reference wrote (Metal forward modes 1-3, train modes) is
+    kept verbatim on rewrite, and none of its rows is read as a gfx950 split
+    count (src/attention_metal.mm:184-336 reads only 7-column F and 8-column
+    T rows, so it skips the HF / HT rows written here)."""
+    ref = tmp_path / "attn_ref.csv"
+    ref_rows = ["F,256,64,0,1,0,3", "F,512,64,1,0,1,1", "T,256,64,1,0,1,1,2"]
+    ref.write_text("#lc_tune_cache,attention,2\n"
+                   "#columns,kind,seq,dim,causal,resident_hint,sync_hint,compute_loss_or_mode,mode\n"
+                   + "\n".join(ref_rows) + "\n", encoding="utf-8")
+    out = tmp_path / "attn_out.csv"
+    _run(f"""
+        import lightning_core as lc
+        lc.attention_tune_cache_load({str(ref)!r})
+        assert lc.attention_tune_cache_size() == 0, lc.attention_tune_cache_size()
+        lc.attention_tune_cache_save({str(out)!r})
+    """, tmp_path)
+    lines = _lines(out)
+    assert lines[0] == "#lc_tune_cache,attention,2"
+    body = [l for l in lines if not l.startswith("#")]
+    assert body == ref_rows
+    # the reference's row filter (exactly 7 columns for F, 8 for T) keeps only its own rows
+    hip_row = "HF,256,64,0,1,0,gfx950,4"
+    cols = hip_row.split(",")
+    assert not ((len(cols) == 7 and cols[0] == "F") or (len(cols) == 8 and cols[0] == "T"))
 
 
 _GETENV = """
