@@ -27,12 +27,14 @@ hipError_t gemmF32(const float* A, const float* B, float* C, int M, int N, int K
                    hipStream_t stream);
 // Workspace and protocol state of the stream-K fp32 GEMM.  `part` holds
 // max_groups * 4096 floats of partial tiles and `flags` max_groups ints;
-// a workgroup publishes its partial by storing `epoch` to its flag, so the
-// caller passes a value no earlier launch over the same flags used (flags
-// start at zero; epochs from 1).  Owners poll a flag at most `spin_limit`
-// times; one whose wait runs out stores 1 to *fail (device-visible memory the
-// caller clears and checks after the stream sync) and that launch's result
-// is invalid.  Launches that share part/flags must not overlap.
+// a workgroup publishes its partial by storing `epoch` to its flag, and the
+// owner clears the flags it saw set, so a launch without a timeout leaves
+// every flag at zero.  The caller passes a new epoch per launch (flags start
+// at zero; epochs from 1), so a flag a timed-out launch left set is never
+// taken for ready later.  Owners poll a flag at most `spin_limit` times; one
+// whose wait runs out stores 1 to *fail (device-visible memory the caller
+// clears and checks after the stream sync) and that launch's result is
+// invalid.  Launches that share part/flags must not overlap.
 struct StreamKSync {
   float* part;
   int* flags;

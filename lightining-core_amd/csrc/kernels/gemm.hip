@@ -1353,9 +1353,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, 
 // and stops waiting: that launch's result is invalid.  Flags carry the
 // launch's epoch, a number the host changes on every launch, so a flag left
 // by an earlier launch (one whose owner gave up before a late publisher set
-// it) never reads as ready; flags are never cleared.  With T a multiple of G
-// (1024^3: 256 tiles on 256 CUs) every range is whole tiles and nothing is
-// published.
+// it) never reads as ready.  Owners clear the flags they saw set, so a launch
+// without a timeout leaves every flag at zero and a replay of a captured
+// launch (same epoch) starts clean.  With T a multiple of G (1024^3: 256
+// tiles on 256 CUs) every range is whole tiles and nothing is published.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done
@@ -1537,6 +1538,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
       while (wf > 0 && begin_of(wf) > t * nk) {
         --wf;
       }
+      int q_ready = rank;  // (wave 0, lane 0) flags [wf, q_ready) were seen set
       if (tid == 0) {
         for (int q = wf; q < rank; ++q) {
           if (begin_of(q) == begin_of(q + 1)) {
@@ -1552,8 +1554,16 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
           if (spin >= sync.spin_limit) {
             // gave up: report, and wait for no further partial
             __hip_atomic_store(sync.fail, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            q_ready = q;
             break;
           }
+        }
+        // Clear the flags seen set, so a launch leaves its flags at zero
+        // (a graph replay reuses the captured epoch).  A flag a late
+        // publisher sets after a timeout keeps this launch's epoch, which no
+        // later launch on these flags waits for.
+        for (int q = wf; q < q_ready; ++q) {
+          __hip_atomic_store(sync.flags + wg_of(q), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
       }
       stage_barrier();
