@@ -342,6 +342,20 @@ lcError_t lcMatMulWithPolicyBatched(const float* a, const float* b, float* out, 
 /* matMulMetalResetTuning (ops_backend.hpp:295): clears the gfx950 tune cache. */
 lcError_t lcMatMulResetTuning(void);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  out = a . b in fp32 with the kernels of lcMatMul, on
+ * device-resident row-major a [m, k], b [k, n], out [m, n]; every other byte
+ * the kernels touch (stream-K partial tiles and flags, zero-padded copies of
+ * an operand whose dims are not multiples of 64 or whose base is not 16-byte
+ * aligned) lives in a fixed 32 MiB static device array that each GPU holds
+ * until the process ends.  Allocates nothing; synchronises the backend stream
+ * before returning.  Padded copies beyond the array (28 MiB for both) ->
+ * LC_NOT_SUPPORTED; pointers HIP does not know as device memory ->
+ * LC_INVALID_VALUE.  All calls on one GPU share the array: the library
+ * serialises its own callers, calls that overlap on one GPU otherwise race. */
+lcError_t lcMatMulDeviceNoAlloc(const float* a, const float* b, float* out, size_t m, size_t k, size_t n);
+
 /* MatMulMetalResidentSession<T> (ops.hpp:1339-1379), with session-owned
  * device buffers and a compute dtype (fp32 host data is rounded to bf16/fp16
  * once at upload, like the reference's fp16 resident batch path,

@@ -170,6 +170,7 @@ SIGNATURES = {
     "lcMatMulWithPolicy": (_E, [BUF, BUF, BUF, c_size, c_size, c_size, c_int, P(MatMulIoPolicyC)]),
     "lcMatMulWithPolicyBatched": (_E, [BUF, BUF, BUF, c_size, c_size, c_size, c_int, P(MatMulIoPolicyC), c_size]),
     "lcMatMulResetTuning": (_E, []),
+    "lcMatMulDeviceNoAlloc": (_E, [c_void_p, c_void_p, c_void_p, c_size, c_size, c_size]),
     "lcMatMulResidentSessionCreate": (_E, [c_size, c_size, c_size, c_int, P(c_void_p)]),
     "lcMatMulResidentSessionDestroy": (_E, [c_void_p]),
     "lcMatMulResidentSessionStart": (_E, [c_void_p, BUF, BUF, BUF]),
