@@ -6,7 +6,7 @@ inputs uploaded and converted once, then launch-only.  One step = one
 8192^3 GEMM launch; the default times the config's 100 iterations.  `value` =
 algorithmic FLOPs (2*M*N*K per step) / wall time of the timed region
 (hipEvents on the backend stream, device synchronised on both sides).
-`roofline` is the dominant kernel, gemm_half_tn_w4_kernel, whose average
+`roofline` is the dominant kernel, gemm_half_tn_w4r_kernel, whose average
 launch time is measured the same way; `cpu_baseline` is the reference's own
 matMulCpu (oracle/_ref/libref.so, single thread) on a row subset of the same
 bf16-rounded operands, scaled by rows (output rows are independent).
@@ -211,7 +211,7 @@ def bench_headline(lc, synth, steps, warmup, cpu):
     # same back-to-back loop, measured on the backend stream
     kms = ms_per_step
     achieved = flops_step / (kms * 1e-3) / 1e12
-    roofline = {"bound": "mfma", "kernel": "gemm_half_tn_w4_kernel<BF16> (8192^3, v_mfma_f32_32x32x16_bf16)",
+    roofline = {"bound": "mfma", "kernel": "gemm_half_tn_w4r_kernel<BF16> (8192^3, v_mfma_f32_32x32x16_bf16)",
                 "achieved": round(achieved, 3), "peak": PEAK_TFLOPS["bf16"], "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_TFLOPS["bf16"], 4), "traffic": GEMM_BF16_8192_TRAFFIC,
                 "avg_kernel_ms": round(kms, 5), "algorithmic_flops_per_launch": int(flops_step),
@@ -493,8 +493,9 @@ PMC_GEMMS = 20
 # FETCH_SIZE: GEMM 12329.9 KiB/dispatch, copy 131084.4 KiB for 262144 KiB moved (x2.000);
 # WRITE_SIZE: GEMM 4096.0 KiB/dispatch, copy 262144.0 KiB (x1.000).
 GEMM_F32_1024_TRAFFIC = 25235186 + 4194304  # HBM bytes per launch (fetch + write, calibrated)
-# 8192^3 bf16 (gemm_half_tn_w4_kernel), profiles/gemm_half_tn_w4_kernel_8192cube_traffic.txt
-GEMM_BF16_8192_TRAFFIC = None
+# 8192^3 bf16 (gemm_half_tn_w4r_kernel), profiles/gemm_half_tn_w4r_kernel_8192cube_traffic.txt
+# FETCH_SIZE 787324.4 KiB/dispatch (x1.9998), WRITE_SIZE 262144.0 KiB (x1.000)
+GEMM_BF16_8192_TRAFFIC = 1612298878 + 268435462
 
 
 def pmc_workload(lc, synth, which="c2"):

@@ -127,7 +127,7 @@ hipError_t convertTransposePad(const float* src, uint16_t* dst, int batch, int r
 // kSmall 64x64, kSkinny for M <= 16; kAuto follows gemmHalfChoose
 // (CJ_HIP_GEMM_TILE=w4|w4d|lds|big8|big4|mid|small overrides it).
 enum class GemmHalfVariant {
-  kAuto = 0, kLds = 1, kBig8 = 2, kBig4 = 3, kMid = 4, kSmall = 5, kSkinny = 6, kW4 = 7, kW4D = 8
+  kAuto = 0, kLds = 1, kBig8 = 2, kBig4 = 3, kMid = 4, kSmall = 5, kSkinny = 6, kW4 = 7, kW4D = 8, kW4R = 9
 };
 GemmHalfVariant gemmHalfChoose(int M, int N);
 hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda, int ldb,

@@ -1098,6 +1098,230 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4d_kernel(const uint16_t* _
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit TN GEMM, 256x256 tile, 4 waves of 128x128 (one per SIMD), fed by a
+// ring of 128-byte-row LDS parts.  A part is 128 rows x 64 k (16 KiB): stage
+// s (k in [64s, 64s + 64)) is parts 4s..4s+3 = A rows 0-127, A rows 128-255,
+// Bt rows 0-127, Bt rows 128-255, and part p lives in ring slot p % 10 (the
+// ring is the whole 160 KiB of LDS).  Each global -> LDS copy moves 8 rows x
+// 128 bytes, whole cache lines: the L1 sends one 128-byte request per row to
+// L2 where the 64-byte rows of gemm_half_tn_w4_kernel's 32-deep slices sent
+// two (counters on 8192^3: 136M L2 read requests against 67M for the same
+// bytes, the address unit stalled on the L1 for 67M cycles).
+//
+// Per stage a wave runs 4 k-steps of 16 MFMAs (32x32x16).  Its 16 copies go
+// to parts 4s+6 .. 4s+9 (the last two parts of stage s+1, the first two of
+// stage s+2), whose slots held stage s-1: the first 8 one after every second
+// MFMA of k-step 0, the rest one after every fourth MFMA of k-steps 1-2.
+// Fragments of k-step j+1 are read during k-step j.  In k-step 3, after its
+// first 8 MFMAs, the wave waits for its own copies of stage s+1 (vmcnt(8):
+// only the 8 copies of stage s+2 may still be in flight) and meets the one
+// barrier of the stage, which makes stage s+1 readable and retires stage s
+// (whose last fragments are already in registers); it then issues the reads
+// of stage s+1's first fragments, which land while the other 8 MFMAs run.  So a copy has at least 2.5
+// k-steps to land, every stage has one barrier and no fragment read waits on
+// one.  Copies past the last stage re-load it into retired slots (unused).
+//
+// The LDS rows carry the 128-byte swizzle of gemm_half_tn_lds_kernel (16-byte
+// chunk c of row r at c ^ ((r >> 1) & 7)): the fragment reads of 16 rows
+// touch every bank once.  The k order of each accumulator is that of the
+// other 256x256 kernels (bit-identical results).  Tiles are ordered in groups
+// of 4 tile rows per XCD.  Operands are padded to 256 rows; lane offsets are
+// 32-bit (the host keeps 256 * ld * 2 bytes below 2^31).
+// ---------------------------------------------------------------------------
+template <typename T, typename Epi>
+__global__ __launch_bounds__(256) void gemm_half_tn_w4r_kernel(const uint16_t* __restrict__ A,
+                                                               const uint16_t* __restrict__ Bt, int M, int N, int K,
+                                                               int lda, int ldb, int tiles_n, Epi epi) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int ROWB = BK * 2;           // bytes per LDS row (128)
+  constexpr int PART = 128 * BK;         // elements per part
+  constexpr int NPART = 10;              // ring slots (160 KiB)
+  __shared__ __attribute__((aligned(16))) uint16_t smem[NPART * PART];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+
+  constexpr int GROUP = 4;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int nwg = gridDim.x;
+  const int full = nwg & ~7;
+  int pid = blockIdx.x;
+  if (pid < full) {
+    pid = (pid & 7) * (full >> 3) + (pid >> 3);
+  }
+  const int group_size = GROUP * tiles_n;
+  const int group = pid / group_size;
+  const int first_m = group * GROUP;
+  const int gm = min(tiles_m - first_m, GROUP);
+  const int in_group = pid - group * group_size;
+  const int bm = (first_m + in_group % gm) * BM;
+  const int bn = (in_group / gm) * BN;
+
+  // Copy instruction i (0..15 per part) fills part rows 8i + lane/8, physical
+  // chunk lane%8; wave w issues i = w + 4j, j = 0..3.
+  const int crow = lane >> 3;
+  const int pch = lane & 7;
+  uint32_t a_off[4];
+  uint32_t b_off[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 8 * (wave + 4 * j) + crow;
+    const int lch = pch ^ ((row >> 1) & 7);
+    a_off[j] = static_cast<uint32_t>(row * lda + lch * 8) * 2u;
+    b_off[j] = static_cast<uint32_t>(row * ldb + lch * 8) * 2u;
+  }
+  const uint16_t* a_tile = A + static_cast<size_t>(bm) * lda;
+  const uint16_t* b_tile = Bt + static_cast<size_t>(bn) * ldb;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = lds_addr(smem);
+  const int S = K / BK;
+  // Copy j (0..3) of part p into slot `slot` (= p % NPART); parts past the
+  // last stage re-load the last stage.
+  auto issue_one = [&](int p, int slot, int j) {
+    const int st = min(p >> 2, S - 1);
+    const int ty = p & 3;
+    const uint32_t dst = lds0 + static_cast<uint32_t>(slot * PART * 2 + (wave_s + 4 * j) * 1024);
+    if (ty < 2) {
+      load_lds16_sbase(a_off[j], a_tile + static_cast<size_t>(ty * 128) * lda + st * BK, dst);
+    } else {
+      load_lds16_sbase(b_off[j], b_tile + static_cast<size_t>((ty - 2) * 128) * ldb + st * BK, dst);
+    }
+  };
+
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  // Fragment f (0..7: A rows for f < 4, then Bt rows) of k-step kk of the
+  // stage whose A / Bt parts of this wave sit in slots sa / sb.
+  auto frag = [&](int sa, int sb, int kk, int f) -> u32x4 {
+    const int slot = f < 4 ? sa : sb;
+    const int row = (f & 3) * 32 + lrow;
+    const int c = 2 * kk + lhalf;
+    const char* base = reinterpret_cast<const char*>(smem + slot * PART);
+    return *reinterpret_cast<const u32x4*>(base + row * ROWB + ((c ^ ((row >> 1) & 7)) << 4));
+  };
+  auto wrap = [](int x) { return x >= NPART ? x - NPART : x; };
+
+  floatx16 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[i][j] = zero16();
+    }
+  }
+
+  // Prologue: stage 0 and the first two parts of stage 1.
+#pragma unroll
+  for (int p = 0; p < 6; ++p) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      issue_one(p, p, j);
+    }
+  }
+  wait_vmcnt<8>();                     // stage 0 has landed
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // no scalar load pending at the loop head
+  stage_barrier();
+  // slot of this stage's first part, and of this wave's A / Bt parts
+  int s0 = 0;
+  const int ta = wm >> 7;
+  const int tb = 2 + (wn >> 7);
+  u32x4 f0[8];
+  u32x4 f1[8];
+#pragma unroll
+  for (int f = 0; f < 8; ++f) {
+    f0[f] = frag(ta, tb, 0, f);
+  }
+  for (int s = 0; s < S; ++s) {
+    const int sa = wrap(s0 + ta);
+    const int sb = wrap(s0 + tb);
+    const int p6 = 4 * s + 6;
+    const int c6 = wrap(s0 + 6);  // slot of part 4s+6; parts 4s+6..4s+9 fill the slots of stage s-1
+    // k-step 0: MFMAs on f0; f1 <- k-step 1; copies of parts 4s+6, 4s+7
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = mfma32x32x16<T>(f0[i >> 2], f0[4 + (i & 3)], acc[i >> 2][i & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        f1[i] = frag(sa, sb, 1, i);
+      }
+      if (i & 1) {
+        const int q = i >> 1;  // 0..7
+        issue_one(p6 + (q >> 2), wrap(c6 + (q >> 2)), q & 3);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // k-step 1: MFMAs on f1; f0 <- k-step 2; copies of part 4s+8
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = mfma32x32x16<T>(f1[i >> 2], f1[4 + (i & 3)], acc[i >> 2][i & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        f0[i] = frag(sa, sb, 2, i);
+      }
+      if ((i & 3) == 3) {
+        issue_one(p6 + 2, wrap(c6 + 2), i >> 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // k-step 2: MFMAs on f0; f1 <- k-step 3; copies of part 4s+9
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = mfma32x32x16<T>(f0[i >> 2], f0[4 + (i & 3)], acc[i >> 2][i & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        f1[i] = frag(sa, sb, 3, i);
+      }
+      if ((i & 3) == 3) {
+        issue_one(p6 + 3, wrap(c6 + 3), i >> 2);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // k-step 3: 8 MFMAs, the stage barrier, then the next stage's first
+    // fragments under the other 8 MFMAs.
+    const int n0 = wrap(s0 + 4);
+    const int na = wrap(n0 + ta);
+    const int nb = wrap(n0 + tb);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      acc[i >> 2][i & 3] = mfma32x32x16<T>(f1[i >> 2], f1[4 + (i & 3)], acc[i >> 2][i & 3]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i == 7) {
+        wait_vmcnt<8>();  // this wave's copies of stage s + 1 have landed
+        stage_barrier();  // everyone's have; stage s is retired
+        // all 8 reads at once, A block 0 and the Bt blocks first (the next
+        // stage's first four MFMAs use them), under the remaining 8 MFMAs
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const int f = q == 0 ? 0 : (q <= 4 ? q + 3 : q - 4);
+          f0[f] = frag(na, nb, 0, f);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    s0 = n0;
+  }
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the wave ends
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = bn + wn + j * 32 + lrow;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = bm + wm + i * 32 + acc_row(r, lane);
+        if (m < M && n < N) {
+          epi(m, n, acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Ring-pipelined 16-bit TN GEMM for short K (the ViT block's GEMMs, K = 768).
 //
 // With K = 768 a tile has 12 stages of BK = 64 and each stage holds only a
@@ -1676,6 +1900,8 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 //          (gemm_half_tn_w4_kernel); needs A / Bt padded to 256 rows
 //   w4d    256x256, 4 waves 2x2, two 64-deep stages, two barriers per stage
 //          (gemm_half_tn_w4d_kernel); needs A / Bt padded to 256 rows
+//   w4r    256x256, 4 waves 2x2, ring of ten 128-byte-row parts, one barrier
+//          per 64-deep stage (gemm_half_tn_w4r_kernel); needs A / Bt padded
 //   lds    256x256, 8 waves 2x4 (128x64 each), global -> LDS direct loads
 //          (gemm_half_tn_lds_kernel); needs A / Bt padded to 256 rows
 //   big8   256x256, 8 waves 2x4, LDS double buffer fed from registers
@@ -1683,13 +1909,15 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 //   mid    128x128, 4 waves 2x2 (64x64 each)
 //   small   64x64,  4 waves 2x2 (32x32 each)
 // Default: the largest tile that still gives at least one workgroup per CU
-// (w4 from two tiles per CU and w4d below that where the operands are padded,
-// big8 elsewhere; measured 8192^3 bf16: w4 1300-1310 against lds 1230-1265
-// TFLOP/s, 4096^3: w4d 1267-1289 against lds 1240-1260 and w4 1220-1230).
+// (w4r from one tile per CU where the operands are padded, big8 elsewhere).
+// Measured with alternating runs on one box, 8192^3 / 4096^3 bf16 TFLOP/s:
+// w4r 1281-1299 / 1271-1280, w4d 1287-1299 / 1263-1269, w4 1281-1289 /
+// 1203-1204; w4r also takes 3.5% fewer cycles at 8192^3 in the counters
+// (half the L2 read requests of w4, L2 latency 268 against 323 cycles).
 // lds stays selectable (tune cache, CJ_HIP_GEMM_TILE).
 // CJ_HIP_GEMM_TILE=<name> overrides the choice (tuning sweeps), like the
 // reference's CJ_* tuning variables.
-enum class HalfTile { kW4, kW4D, kLds, kBig8, kBig4, kMid, kSmall };
+enum class HalfTile { kW4, kW4D, kW4R, kLds, kBig8, kBig4, kMid, kSmall };
 
 inline int tiles_for(int M, int N, int b) { return ((M + b - 1) / b) * ((N + b - 1) / b); }
 
@@ -1698,6 +1926,7 @@ inline HalfTile pick_half_tile(int M, int N, bool padded) {
     const std::string v(env);
     if (v == "w4" && padded) return HalfTile::kW4;
     if (v == "w4d" && padded) return HalfTile::kW4D;
+    if (v == "w4r" && padded) return HalfTile::kW4R;
     if (v == "lds" && padded) return HalfTile::kLds;
     if (v == "big8") return HalfTile::kBig8;
     if (v == "big4") return HalfTile::kBig4;
@@ -1705,11 +1934,8 @@ inline HalfTile pick_half_tile(int M, int N, bool padded) {
     if (v == "small") return HalfTile::kSmall;
   }
   constexpr int kCUs = 256;
-  if (tiles_for(M, N, 256) >= 2 * kCUs) {
-    return padded ? HalfTile::kW4 : HalfTile::kBig8;
-  }
   if (tiles_for(M, N, 256) >= kCUs) {
-    return padded ? HalfTile::kW4D : HalfTile::kBig8;
+    return padded ? HalfTile::kW4R : HalfTile::kBig8;
   }
   if (tiles_for(M, N, 128) >= kCUs) {
     return HalfTile::kMid;
@@ -1733,6 +1959,7 @@ static hipError_t launch_gemm_half_tile(HalfTile tile, LoadA load_a, const uint1
   switch (tile) {
     case HalfTile::kW4:
     case HalfTile::kW4D:
+    case HalfTile::kW4R:
     case HalfTile::kLds:
     case HalfTile::kBig8:
       return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
@@ -1771,12 +1998,16 @@ inline bool vit_ring_enabled() {
 // Its copies use 32-bit byte offsets from a stage base and 16-byte alignment.
 inline bool ring_fits(long long rows, long long ld) { return rows * ld * 2 < (1LL << 31) && ld % 8 == 0; }
 
-template <typename T, bool DOUBLE>
+// W4: 0 = gemm_half_tn_w4_kernel, 1 = gemm_half_tn_w4d_kernel, 2 = gemm_half_tn_w4r_kernel
+template <typename T, int W4>
 static hipError_t launch_gemm_w4(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda,
                                  int ldb, int ldc, hipStream_t stream) {
   const int tiles_n = (N + 255) / 256;
   const dim3 grid(((M + 255) / 256) * tiles_n);
-  if constexpr (DOUBLE) {
+  if constexpr (W4 == 2) {
+    hipLaunchKernelGGL((gemm_half_tn_w4r_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
+                       tiles_n, EpiF32{C, ldc});
+  } else if constexpr (W4 == 1) {
     hipLaunchKernelGGL((gemm_half_tn_w4d_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
                        tiles_n, EpiF32{C, ldc});
   } else {
@@ -1874,6 +2105,7 @@ GemmHalfVariant gemmHalfChoose(int M, int N) {
   switch (pick_half_tile(M, N, true)) {
     case HalfTile::kW4: return GemmHalfVariant::kW4;
     case HalfTile::kW4D: return GemmHalfVariant::kW4D;
+    case HalfTile::kW4R: return GemmHalfVariant::kW4R;
     case HalfTile::kLds: return GemmHalfVariant::kLds;
     case HalfTile::kBig8: return GemmHalfVariant::kBig8;
     case HalfTile::kBig4: return GemmHalfVariant::kBig4;
@@ -1895,17 +2127,22 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
   }
   // A and Bt come from the resident upload, padded to 256 rows; the copies'
   // 32-bit lane offsets reach 256 rows of either operand.
-  if ((variant == GemmHalfVariant::kLds || variant == GemmHalfVariant::kW4 || variant == GemmHalfVariant::kW4D) &&
+  if ((variant == GemmHalfVariant::kLds || variant == GemmHalfVariant::kW4 || variant == GemmHalfVariant::kW4D ||
+       variant == GemmHalfVariant::kW4R) &&
       (256LL * lda * 2 >= (1LL << 31) || 256LL * ldb * 2 >= (1LL << 31))) {
     variant = GemmHalfVariant::kBig8;
   }
   if (variant == GemmHalfVariant::kW4 && K > 0) {
-    return t == Half::kBF16 ? launch_gemm_w4<BF16, false>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
-                            : launch_gemm_w4<F16, false>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
+    return t == Half::kBF16 ? launch_gemm_w4<BF16, 0>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
+                            : launch_gemm_w4<F16, 0>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
   }
   if (variant == GemmHalfVariant::kW4D && K > 0) {
-    return t == Half::kBF16 ? launch_gemm_w4<BF16, true>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
-                            : launch_gemm_w4<F16, true>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
+    return t == Half::kBF16 ? launch_gemm_w4<BF16, 1>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
+                            : launch_gemm_w4<F16, 1>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
+  }
+  if (variant == GemmHalfVariant::kW4R && K > 0) {
+    return t == Half::kBF16 ? launch_gemm_w4<BF16, 2>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
+                            : launch_gemm_w4<F16, 2>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
   }
   if (variant == GemmHalfVariant::kLds && K > 0) {
     return t == Half::kBF16 ? launch_gemm_lds<BF16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)

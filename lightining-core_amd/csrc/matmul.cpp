@@ -93,6 +93,7 @@ constexpr VariantInfo kF32Variants[] = {
 constexpr VariantInfo kHalfVariants[] = {
     {static_cast<int>(kern::GemmHalfVariant::kW4), "half_w4_256x256", 256, 256, 32, 4, 1},
     {static_cast<int>(kern::GemmHalfVariant::kW4D), "half_w4d_256x256", 256, 256, 64, 4, 1},
+    {static_cast<int>(kern::GemmHalfVariant::kW4R), "half_w4r_256x256", 256, 256, 64, 4, 1},
     {static_cast<int>(kern::GemmHalfVariant::kLds), "half_lds_256x256", 256, 256, 64, 8, 1},
     {static_cast<int>(kern::GemmHalfVariant::kBig8), "half_big8_256x256", 256, 256, 64, 8, 1},
     {static_cast<int>(kern::GemmHalfVariant::kBig4), "half_big4_256x256", 256, 256, 64, 4, 1},
