@@ -733,6 +733,29 @@ __global__ __launch_bounds__(1024) void mse_loss_kernel(const float* __restrict_
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A 16-bit value as fp32.
+template <typename T>
+__device__ __forceinline__ float half_bits_to_f32(uint32_t h);
+template <>
+__device__ __forceinline__ float half_bits_to_f32<BF16>(uint32_t h) {
+  return __builtin_bit_cast(float, (h & 0xffffu) << 16);
+}
+template <>
+__device__ __forceinline__ float half_bits_to_f32<F16>(uint32_t h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h & 0xffffu)));
+}
+
+// Eight packed 16-bit values times c, rounded back (RNE).
+template <typename T>
+__device__ __forceinline__ u32x4 scale_halves(u32x4 v, float c) {
+  u32x4 r;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    r[w] = pack2<T>(half_bits_to_f32<T>(v[w]) * c, half_bits_to_f32<T>(v[w] >> 16) * c);
+  }
+  return r;
+}
+
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* __restrict__ Q,
                                                                const uint16_t* __restrict__ K,
@@ -799,10 +822,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
     }
   };
 
+  // Q fragments, pre-multiplied by c = scale * log2(e) (rounded back to the
+  // 16-bit type once per wave), so the QK^T MFMAs produce scores in exp2 units.
+  const float c = scale * kLog2e;
   u32x4 qf[QS];
 #pragma unroll
   for (int s = 0; s < QS; ++s) {
-    qf[s] = *reinterpret_cast<const u32x4*>(Qh + static_cast<size_t>(q0 + lrow) * D + s * 16 + 8 * half);
+    qf[s] = scale_halves<T>(
+        *reinterpret_cast<const u32x4*>(Qh + static_cast<size_t>(q0 + lrow) * D + s * 16 + 8 * half), c);
   }
 
   // Fragment addresses (elements).  K: MFMA row lrow of 32-key block kt reads
@@ -828,10 +855,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   for (int t = 0; t < DT; ++t) {
     o[t] = zero16();
   }
-  float m_run = kMaskValue;
+  // Scores are kept relative to a per-query reference m_run (exp2 units): the
+  // QK^T MFMAs start from -m_run instead of zero, so x = s*c - m_run comes
+  // out of the accumulator and p = exp2(x) needs no extra arithmetic.  The
+  // reference moves to the tile max on a query's first tile with a valid key,
+  // and later only when the max exceeds it by more than 8 (then O, l and the
+  // tile's scores are shifted); exponents stay <= 8.
+  float m_run = 0.0f;
   float l_run = 0.0f;
+  bool started = false;
   const int qi = q0 + lrow;
-  const float c = scale * kLog2e;
   const int kend = causal ? min(S, qb * 128 + 128) : S;
   const int nt = (kend + KT - 1) / KT;
   // Causal: tile j is skipped by a wave whose queries all precede its keys
@@ -869,19 +902,29 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
       }
     }
     mt = max_xor32(mt);
-    // Rescale O and l only when some lane's max grew by more than 8 (exp2
-    // units); otherwise keep the stale reference max.  O and l always share
-    // the same reference, so O/l is unchanged; exponents stay <= 8.
-    const float m_cand = fmaxf(m_run, mt);
-    if (__any((m_cand - m_run) * c > 8.0f)) {
-      const float alpha = fast_exp2((m_run - m_cand) * c);
-      m_run = m_cand;
+    // Lanes l and l ^ 32 hold the same query and see the same mt, so their
+    // references stay equal.  O and l always share the reference, so O/l is
+    // unchanged by a shift.
+    const bool valid = mt > 0.5f * kMaskValue;
+    const bool shift = valid && (!started || mt > 8.0f);
+    started = started || valid;
+    if (__any(shift)) {
+      const float sh = shift ? mt : 0.0f;
+      const float alpha = fast_exp2(-sh);
+      m_run += sh;
       l_run *= alpha;
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           o[t][i] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          s_cur[kt][i] -= sh;
         }
       }
     }
@@ -892,7 +935,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
     // clocks while the wave issues the group's VALU work behind it.
     constexpr int NQK = 2 * QS;
     constexpr int EPM = 32 / NQK;
-    const float mc = m_run * c;
+    floatx16 negm;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      negm[i] = -m_run;
+    }
     float ls = 0.0f;
     u32x4 pb[4];
     const uint16_t* ksn = smem + ((j + 1) & 1) * TILE;
@@ -914,13 +961,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
       {
         const int kt = g / QS;
         const int s = g - kt * QS;
-        s_nxt[kt] = mfma32x32x16<T>(kf[g % 3], qf[s], s == 0 ? zero16() : s_nxt[kt]);
+        s_nxt[kt] = mfma32x32x16<T>(kf[g % 3], qf[s], s == 0 ? negm : s_nxt[kt]);
       }
 #pragma unroll
       for (int e = 0; e < EPM; e += 2) {
         const int idx = g * EPM + e;  // score element idx and idx + 1
-        const float p0 = fast_exp2(__builtin_fmaf(s_cur[idx >> 4][idx & 15], c, -mc));
-        const float p1 = fast_exp2(__builtin_fmaf(s_cur[idx >> 4][(idx & 15) + 1], c, -mc));
+        const float p0 = fast_exp2(s_cur[idx >> 4][idx & 15]);
+        const float p1 = fast_exp2(s_cur[idx >> 4][(idx & 15) + 1]);
         const uint32_t pair = pack2<T>(p0, p1);
         // l sums the rounded probabilities the P.V MFMAs consume.
         ls = add_pair<T>(pair, ls);
