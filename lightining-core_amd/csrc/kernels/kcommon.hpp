@@ -126,10 +126,22 @@ __device__ __forceinline__ floatx16 zero16() {
 //    next one.  Callers wait for these copies with explicit vmcnt.
 // `lds` and `sbase` must be wave-uniform.  The LDS address reaches M0 through
 // an "{m0}" input operand, so the compiler itself writes M0 (and knows its
-// value afterwards); the asm never writes M0.  The s_nop covers the one wait
-// state an M0 write needs before an LDS-DMA load reads it.
+// value afterwards); the asm never writes M0.
+// Hazards: the compiler pads its own instructions for hardware hazards but not
+// the contents of an asm statement.  A VALU write of an SGPR (v_readlane /
+// v_readfirstlane, e.g. when the compiler reloads a spilled SGPR into the base
+// pair) needs 5 wait states before a VMEM instruction reads that SGPR; with
+// fewer the load can take a stale half of the 64-bit base and fault.  So the
+// asm first copies the base with an SALU move (SALU reads of VALU-written
+// SGPRs are interlocked) and the load reads the copy; that move is also the
+// one wait state an SALU write of M0 needs before an LDS-DMA load reads M0.
+// (tests/test_asm_hazards.py scans the built kernels for both.)
 __device__ __forceinline__ void load_lds16_sbase(uint32_t voff, const void* sbase, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds) : "memory");
+  uint64_t base;
+  asm volatile("s_mov_b64 %0, %2\n\tglobal_load_lds_dwordx4 %1, %0"
+               : "=&s"(base)
+               : "v"(voff), "s"(sbase), "{m0}"(lds)
+               : "memory");
 }
 
 // LDS byte address of a __shared__ object, as a wave-uniform value.
