@@ -124,14 +124,31 @@ hipError_t convertTransposePad(const float* src, uint16_t* dst, int batch, int r
 // with 4 waves and a ring of 32-deep k slices, kW4D the same waves over two
 // 64-deep stages, kLds 256x256 with 8 waves, all three with direct
 // global->LDS loads; kBig8 / kBig4 256x256 with 8 / 4 waves, kMid 128x128,
-// kSmall 64x64, kSkinny for M <= 16; kAuto follows gemmHalfChoose
+// kSmall 64x64, kSkinny for M <= 16 (split-K when given a SkinnyWork);
+// kAuto follows gemmHalfChoose
 // (CJ_HIP_GEMM_TILE=w4|w4d|lds|big8|big4|mid|small overrides it).
 enum class GemmHalfVariant {
   kAuto = 0, kLds = 1, kBig8 = 2, kBig4 = 3, kMid = 4, kSmall = 5, kSkinny = 6, kW4 = 7, kW4D = 8, kW4R = 9
 };
 GemmHalfVariant gemmHalfChoose(int M, int N);
+// Workspace of the skinny GEMM's split-K: partial tiles (max_splits x
+// max_tiles x kSkinnyPartFloats floats) and one counter per column tile of
+// 64 (zero at allocation; every launch leaves them at zero).  Launches that
+// share it must not overlap.  cus: workgroups to aim for.
+constexpr int kSkinnyMaxSplits = 8;
+constexpr int kSkinnyPartFloats = 1024;  // one 16 x 64 fp32 partial
+struct SkinnyWork {
+  float* part;
+  int* counters;
+  int max_tiles;
+  int max_splits;
+  int cus;
+};
+// k-splits the skinny GEMM uses for N x K.
+int skinnySplits(int N, int K, int cus);
 hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda, int ldb,
-                      int ldc, Half t, GemmHalfVariant variant, hipStream_t stream);
+                      int ldc, Half t, GemmHalfVariant variant, hipStream_t stream,
+                      const SkinnyWork* skinny = nullptr);
 // Same GEMM with a 16-bit output (optionally ReLU).
 hipError_t gemmHalfTNHalfOut(const uint16_t* A, const uint16_t* Bt, uint16_t* C, int M, int N, int K, int lda,
                              int ldb, int ldc, int relu, Half t, hipStream_t stream);

@@ -483,11 +483,23 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_kernel(LoadA load_a,
 }
 
 // ---------------------------------------------------------------------------
-// Skinny 16-bit GEMM (M <= 16): HBM-bound on streaming Bt once.  Each
-// workgroup owns NT 16-column tiles; its 4 waves take interleaved 32-wide
-// k-steps (so together they read 256 contiguous bytes of each Bt row per
-// round) with v_mfma_f32_16x16x32_*, and the 4 partial tiles are summed
-// through LDS.  A (16 rows) is re-read per tile from L2.
+// Skinny 16-bit GEMM (M <= 16): HBM-bound on streaming Bt once.
+//
+// A workgroup owns NR = 16*NT rows of Bt (columns of C) and one of KS
+// contiguous k-ranges (split-K, grid.y).  Rows are staged in LDS by
+// LDS-DMA in k-blocks of 256: each copy instruction reads 1 KB of global
+// memory contiguously (two rows x 512 bytes), which is what lets HBM stream
+// near its peak (the MFMA-layout loads of 16 rows x 64 bytes stop near 5
+// TB/s).  The 16 rows of A ride along in the same stages.  Within a row the
+// 16-byte chunks are XOR-swizzled by (row & 15), so the 16 rows of an MFMA
+// fragment read sit in distinct LDS banks.  Two stages: block b+1 loads
+// while block b is multiplied (v_mfma_f32_16x16x32, the W waves taking the
+// block's 32-wide k-steps in turn).  The W partial tiles are summed through
+// LDS (over the stages, all reads done).  With KS > 1 each workgroup stores
+// its partial to the workspace with device-scope stores, waits for them,
+// and bumps its column tile's counter; the one that brings it to KS sums the
+// KS partials in k order (deterministic), writes C and resets the counter to
+// zero for the next launch.  No workgroup ever waits for another.
 //   16x16x32 layout: A[m = l%16][k = 8(l/16)+j], B[k = 8(l/16)+j][n = l%16],
 //   D[m = 4(l/16) + i][n = l%16], i = 0..3.
 // ---------------------------------------------------------------------------
@@ -504,83 +516,163 @@ __device__ __forceinline__ floatx4 mfma16x16x32<F16>(u32x4 a, u32x4 b, floatx4 c
                                                 0);
 }
 
-template <typename T, int NT, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void gemm_skinny_kernel(const uint16_t* __restrict__ A,
-                                                                  const uint16_t* __restrict__ Bt,
-                                                                  float* __restrict__ C, int M, int N, int K,
-                                                                  int lda, int ldb, int ldc) {
-  __shared__ floatx4 red[WAVES][NT][64];
+constexpr int kSkinnyNT = 4;     // 16-column tiles per workgroup
+constexpr int kSkinnyWaves = 8;
+constexpr int kSkinnyStages = 2;
+constexpr int kSkinnyKB = 256;   // k per stage
+
+template <typename T, int NT, int W, int S>
+__global__ __launch_bounds__(W * 64) void gemm_skinny_kernel(const uint16_t* __restrict__ A,
+                                                              const uint16_t* __restrict__ Bt,
+                                                              float* __restrict__ C, int M, int N, int K, int lda,
+                                                              int ldb, int ldc, float* __restrict__ part,
+                                                              int* __restrict__ counters) {
+  constexpr int NR = 16 * NT;              // Bt rows per workgroup
+  constexpr int ROWS = NR + 16;            // + the 16 rows of A
+  constexpr int KB = kSkinnyKB;
+  constexpr int STAGE = ROWS * KB;         // elements per stage
+  constexpr int PAIRS = ROWS / 2 / W;      // copy instructions per wave per stage
+  static_assert((ROWS / 2) % W == 0 && (NR / 2) % W == 0, "row pairs per wave");
+  static_assert(W >= NT, "one wave per column tile in the final sum");
+  static_assert(W * NT * 1024 + 16 <= S * STAGE * 2, "partials and flag fit over the stages");
+  __shared__ __attribute__((aligned(16))) uint16_t sm[S * STAGE];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int n0 = blockIdx.x * 16 * NT;
-  const int r16 = lane & 15;
-  const int kofs = 8 * (lane >> 4);
-  const uint16_t* arow = A + static_cast<size_t>(r16) * lda + kofs;
-  const uint16_t* brow[NT];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ct = blockIdx.x;
+  const int ks = blockIdx.y;
+  const int KS = gridDim.y;
+  const int n0 = ct * NR;
+  const uint32_t lds0 = lds_addr(sm);
+  const int nkb = (K + KB - 1) / KB;
+  const int per = (nkb + KS - 1) / KS;
+  const int kb0 = min(nkb, ks * per);
+  const int kb1 = min(nkb, kb0 + per);
+  // Copy of k-block kb into stage st: instruction i of wave w fills rows
+  // 2p, 2p+1 (p = w + W*i; Bt rows first, then A's); lane l reads 16 bytes of
+  // row 2p + l/32 at logical chunk (l%32) ^ (row & 15), which lands at
+  // physical chunk l%32.  Chunks past K are not read.
+  auto issue = [&](int kb, int st) {
+    const int k0 = kb * KB;
+    const int valid = min(KB, K - k0) / 8;
 #pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    brow[t] = Bt + static_cast<size_t>(n0 + t * 16 + r16) * ldb + kofs;
-  }
+    for (int i = 0; i < PAIRS; ++i) {
+      const int r0 = 2 * (wave + W * i);
+      const bool is_b = i < NR / 2 / W;
+      const uint16_t* src = is_b ? Bt + static_cast<size_t>(n0 + r0) * ldb : A + static_cast<size_t>(r0 - NR) * lda;
+      const int ld = is_b ? ldb : lda;
+      const int rr = r0 + (lane >> 5);
+      const int chunk = (lane & 31) ^ (rr & 15);
+      if (chunk < valid) {
+        load_lds16_sbase(static_cast<uint32_t>(((lane >> 5) * ld + k0 + chunk * 8) * 2), src,
+                         lds0 + 2u * static_cast<uint32_t>(st * STAGE + r0 * KB));
+      }
+    }
+  };
   floatx4 acc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     acc[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   }
-  // Waves take interleaved 32-wide k-steps: wave w handles w, w+WAVES, ...
-  const int steps = K / 32;
-  int s = wave;
-  for (; s + 3 * WAVES < steps; s += 4 * WAVES) {
-    u32x4 a[4];
-    u32x4 b[4][NT];
+  const int r16 = lane & 15;
+  const int cg = lane >> 4;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      a[u] = *reinterpret_cast<const u32x4*>(arow + (s + WAVES * u) * 32);
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        b[u][t] = *reinterpret_cast<const u32x4*>(brow[t] + (s + WAVES * u) * 32);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        acc[t] = mfma16x16x32<T>(a[u], b[u][t], acc[t]);
-      }
+  for (int p = 0; p < S - 1; ++p) {
+    if (kb0 + p < kb1) {
+      issue(kb0 + p, p);
     }
   }
-  for (; s < steps; s += WAVES) {
-    const u32x4 a = *reinterpret_cast<const u32x4*>(arow + s * 32);
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      acc[t] = mfma16x16x32<T>(a, *reinterpret_cast<const u32x4*>(brow[t] + s * 32), acc[t]);
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int sl = kb - kb0;
+    if (kb + S - 1 < kb1) {
+      issue(kb + S - 1, (sl + S - 1) % S);
+      wait_vmcnt<(S - 1) * PAIRS>();  // this wave's copies of block kb have landed
+    } else {
+      wait_vmcnt<0>();
     }
+    stage_barrier();  // everyone's have
+    const uint16_t* st = sm + (sl % S) * STAGE;
+    const int steps = min(KB, K - kb * KB) / 32;
+    for (int s = wave; s < steps; s += W) {
+      const int ch = 4 * s + cg;  // logical 16-byte chunk of this lane's 8 k
+      const u32x4 a = *reinterpret_cast<const u32x4*>(st + (NR + r16) * KB + ((ch ^ r16) << 3));
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        const int r = t * 16 + r16;
+        const u32x4 b = *reinterpret_cast<const u32x4*>(st + r * KB + ((ch ^ (r & 15)) << 3));
+        acc[t] = mfma16x16x32<T>(a, b, acc[t]);
+      }
+    }
+    stage_barrier();  // the stage is refilled next
   }
+  floatx4* red = reinterpret_cast<floatx4*>(sm);  // [W][NT][64]
+  int* last = reinterpret_cast<int*>(sm + W * NT * 512);
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    red[wave][t][lane] = acc[t];
+    red[(wave * NT + t) * 64 + lane] = acc[t];
   }
   __syncthreads();
+  floatx4 v = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
   if (wave < NT) {
-    const int t = wave;
-    floatx4 v = red[0][t][lane];
+    v = red[wave * 64 + lane];
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) {
-      const floatx4 o = red[w][t][lane];
+    for (int w = 1; w < W; ++w) {
+      const floatx4 o = red[(w * NT + wave) * 64 + lane];
       v[0] += o[0];
       v[1] += o[1];
       v[2] += o[2];
       v[3] += o[3];
     }
-    const int n = n0 + t * 16 + r16;
+  }
+  auto store_c = [&](const floatx4& x) {
+    const int n = n0 + wave * 16 + r16;
     if (n < N) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int m = 4 * (lane >> 4) + i;
+        const int m = 4 * cg + i;
         if (m < M) {
-          C[static_cast<size_t>(m) * ldc + n] = v[i];
+          C[static_cast<size_t>(m) * ldc + n] = x[i];
         }
       }
     }
+  };
+  if (KS == 1) {
+    if (wave < NT) {
+      store_c(v);
+    }
+    return;
+  }
+  // Partial of (ct, ks) at part[((ct * KS + ks) * NT + t) * 256 + i * 64 + lane].
+  // Device-scope (sc1) stores and loads are coherent across the XCDs' L2s;
+  // the vmcnt wait orders the stores before the counter bump.
+  if (wave < NT) {
+    float* mine = part + (static_cast<size_t>(ct * KS + ks) * NT + wave) * 256 + lane;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __hip_atomic_store(mine + i * 64, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    *last = __hip_atomic_fetch_add(counters + ct, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == KS - 1;
+  }
+  __syncthreads();
+  if (*last == 0) {
+    return;
+  }
+  if (wave < NT) {
+    floatx4 x = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k2 = 0; k2 < KS; ++k2) {
+      const float* theirs = part + (static_cast<size_t>(ct * KS + k2) * NT + wave) * 256 + lane;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[i] += __hip_atomic_load(theirs + i * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    store_c(x);
+  }
+  if (threadIdx.x == 0) {
+    __hip_atomic_store(counters + ct, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -2114,8 +2206,19 @@ GemmHalfVariant gemmHalfChoose(int M, int N) {
   }
 }
 
+int skinnySplits(int N, int K, int cus) {
+  const int tiles = (N + 16 * kSkinnyNT - 1) / (16 * kSkinnyNT);
+  const int kblocks = (K + kSkinnyKB - 1) / kSkinnyKB;
+  // Enough workgroups to cover the CUs, at least two k-blocks per split.
+  int splits = 1;
+  while (splits < kSkinnyMaxSplits && tiles * splits < std::max(cus, 1) && kblocks / (splits * 2) >= 2) {
+    splits *= 2;
+  }
+  return splits;
+}
+
 hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda, int ldb, int ldc,
-                      Half t, GemmHalfVariant variant, hipStream_t stream) {
+                      Half t, GemmHalfVariant variant, hipStream_t stream, const SkinnyWork* skinny) {
   if (K % kHBK != 0) {
     return hipErrorInvalidValue;
   }
@@ -2149,16 +2252,23 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
                             : launch_gemm_lds<F16, 2, 4>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
   }
   if (variant == GemmHalfVariant::kSkinny) {
-    // Bt must be readable up to roundup(N, 32) rows (callers pad to 256).
-    constexpr int NT = 2;
-    constexpr int WAVES = 4;
-    const dim3 grid((N + 16 * NT - 1) / (16 * NT));
+    // Bt must be readable up to roundup(N, 64) rows and A up to 16 rows
+    // (callers pad both to 256); split-K needs the workspace.
+    const int tiles = (N + 16 * kSkinnyNT - 1) / (16 * kSkinnyNT);
+    int splits = 1;
+    if (skinny != nullptr && skinny->part != nullptr && skinny->counters != nullptr && tiles <= skinny->max_tiles) {
+      splits = skinnySplits(N, K, skinny->cus);
+      splits = std::min(splits, skinny->max_splits);
+    }
+    const dim3 grid(tiles, splits);
+    float* part = splits > 1 ? skinny->part : nullptr;
+    int* counters = splits > 1 ? skinny->counters : nullptr;
     if (t == Half::kBF16) {
-      hipLaunchKernelGGL((gemm_skinny_kernel<BF16, NT, WAVES>), grid, dim3(WAVES * 64), 0, stream, A, Bt, C, M, N, K,
-                         lda, ldb, ldc);
+      hipLaunchKernelGGL((gemm_skinny_kernel<BF16, kSkinnyNT, kSkinnyWaves, kSkinnyStages>), grid,
+                         dim3(kSkinnyWaves * 64), 0, stream, A, Bt, C, M, N, K, lda, ldb, ldc, part, counters);
     } else {
-      hipLaunchKernelGGL((gemm_skinny_kernel<F16, NT, WAVES>), grid, dim3(WAVES * 64), 0, stream, A, Bt, C, M, N, K,
-                         lda, ldb, ldc);
+      hipLaunchKernelGGL((gemm_skinny_kernel<F16, kSkinnyNT, kSkinnyWaves, kSkinnyStages>), grid,
+                         dim3(kSkinnyWaves * 64), 0, stream, A, Bt, C, M, N, K, lda, ldb, ldc, part, counters);
     }
     return hipGetLastError();
   }

@@ -135,6 +135,9 @@ struct HipContext {
   DeviceBuffer gemm_part, gemm_flags;
   PinnedBuffer gemm_fail;
   int gemm_epoch = 0;
+  // Split-K workspace of the skinny 16-bit GEMM (partials + per-column-tile
+  // counters, zero at allocation and after every launch); `stream` only.
+  DeviceBuffer skinny_part, skinny_counters;
 };
 
 bool hipAvailable();

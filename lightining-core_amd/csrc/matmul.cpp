@@ -99,7 +99,7 @@ constexpr VariantInfo kHalfVariants[] = {
     {static_cast<int>(kern::GemmHalfVariant::kBig4), "half_big4_256x256", 256, 256, 64, 4, 1},
     {static_cast<int>(kern::GemmHalfVariant::kMid), "half_mid_128x128", 128, 128, 64, 4, 1},
     {static_cast<int>(kern::GemmHalfVariant::kSmall), "half_small_64x64", 64, 64, 64, 4, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kSkinny), "half_skinny_16x32", 16, 32, 32, 4, 4},
+    {static_cast<int>(kern::GemmHalfVariant::kSkinny), "half_skinny_16x64", 16, 64, 256, 8, 2},
 };
 
 struct VariantTable {
@@ -171,8 +171,20 @@ hipError_t launchGemm(HipContext* ctx, MatMulResident& r, int variant) {
                                static_cast<kern::GemmF32Variant>(variant), ctx->stream);
   }
   const int kp = static_cast<int>(roundUp(r.k, kern::kHalfGemmBK));
+  kern::SkinnyWork skinny{nullptr, nullptr, 0, 0, 0};
+  if (M <= 16) {
+    const int tiles = static_cast<int>(roundUp(r.n, 64) / 64);
+    if (ctx->skinny_part.ensure(static_cast<std::size_t>(kern::kSkinnyMaxSplits) * tiles * kern::kSkinnyPartFloats *
+                                sizeof(float)) != Status::kSuccess ||
+        ctx->skinny_counters.ensure(static_cast<std::size_t>(tiles) * sizeof(int), true) != Status::kSuccess) {
+      return hipErrorOutOfMemory;
+    }
+    skinny = kern::SkinnyWork{ctx->skinny_part.as<float>(), ctx->skinny_counters.as<int>(),
+                              static_cast<int>(ctx->skinny_counters.size() / sizeof(int)), kern::kSkinnyMaxSplits,
+                              ctx->props.multiProcessorCount > 0 ? ctx->props.multiProcessorCount : 256};
+  }
   return kern::gemmHalfTN(r.a.as<uint16_t>(), r.b.as<uint16_t>(), r.c.as<float>(), M, N, kp, kp, kp, N,
-                          halfOf(r.dtype), static_cast<kern::GemmHalfVariant>(variant), ctx->stream);
+                          halfOf(r.dtype), static_cast<kern::GemmHalfVariant>(variant), ctx->stream, &skinny);
 }
 
 // Times the candidates round-robin (so clock and thermal drift spread over

@@ -119,6 +119,30 @@ def test_matmul_bf16_skinny_config5(lc, oracle):
     assert_parity(ref, got, "bf16", "bf16 skinny 16x8192x8192")
 
 
+@pytest.mark.parametrize("m,k,n", [(16, 1000, 3000), (5, 960, 777), (16, 4096, 2048), (1, 2048, 130),
+                                   (16, 320, 8192)])
+def test_matmul_bf16_skinny_split_k(lc, oracle, m, k, n):
+    """The skinny GEMM's split-K paths: ragged N (column tiles of 64) and K
+    (a last k-block shorter than 256), M < 16, 1 to 8 splits.  Three
+    launches on one session and a second session of the same shape must all
+    match: the last workgroup of each column tile resets its counter, so a
+    launch never sees another's counts."""
+    a = synth.normal((m, k), stream=11)
+    b = synth.normal((k, n), stream=12)
+    ref = oracle.matmul(synth.round_bf16(a), synth.round_bf16(b))
+    note(f"[case] skinny split-K {m}x{k}x{n}")
+    s = lc.MatMulResidentSession(m, k, n, "bf16")
+    s.start_into(a, b)
+    first = s.finish_into().reshape(m, n).copy()
+    assert_parity(ref, first, "bf16", f"bf16 skinny {m}x{k}x{n}")
+    s2 = lc.MatMulResidentSession(m, k, n, "bf16")
+    s2.start_into(a, b)
+    s2.run_batch_sync_cached_no_download(3)
+    again = s2.finish_into().reshape(m, n)
+    # same partials, same k order: bit-identical
+    np.testing.assert_array_equal(again, first)
+
+
 def test_resident_session_protocol(lc, oracle):
     m, k, n = 96, 80, 72
     a = synth.uniform((m, k), stream=9)

@@ -92,14 +92,14 @@ HALF_CASES = [("half_w4_256x256", (300, 129, 200)), ("half_w4_256x256", (520, 25
               ("half_w4r_256x256", (700, 1000, 513)),
               ("half_lds_256x256", (300, 129, 200)), ("half_big8_256x256", (300, 129, 200)),
               ("half_big4_256x256", (520, 256, 130)), ("half_mid_128x128", (77, 320, 513)),
-              ("half_small_64x64", (1000, 777, 1030)), ("half_skinny_16x32", (9, 200, 300))]
+              ("half_small_64x64", (1000, 777, 1030)), ("half_skinny_16x64", (9, 200, 300))]
 _TILES = {"f32_dp_64x64x64": "64,64,64,8,2", "f32_streamk_64x64x64": "64,64,64,8,2",
           "f32_dp_64x64x32": "64,64,32,8,2", "half_w4_256x256": "256,256,32,4,1",
           "half_w4d_256x256": "256,256,64,4,1", "half_w4r_256x256": "256,256,64,4,1",
           "half_lds_256x256": "256,256,64,8,1",
           "half_big8_256x256": "256,256,64,8,1", "half_big4_256x256": "256,256,64,4,1",
           "half_mid_128x128": "128,128,64,4,1", "half_small_64x64": "64,64,64,4,1",
-          "half_skinny_16x32": "16,32,32,4,4"}
+          "half_skinny_16x64": "16,64,256,8,2"}
 
 
 @pytest.mark.parametrize("dtype,cases", [("f32", F32_CASES), ("bf16", HALF_CASES), ("f16", HALF_CASES)])

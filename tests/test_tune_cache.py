@@ -59,7 +59,7 @@ def test_matmul_cache_v2_round_trip_and_bad_rows(tmp_path):
         "#columns,m,k,n,dtype,arch,kernel,tile_m,tile_n,tile_k,waves,split_k",
         "1024,1024,1024,0,gfx950,f32_dp_64x64x64,64,64,64,8,2",
         "4096,4096,4096,1,gfx950,half_lds_256x256,256,256,64,8,1",
-        "12,13,14,2,gfx950,half_skinny_16x32,16,32,32,4,4",
+        "12,13,14,2,gfx950,half_skinny_16x64,16,64,256,8,2",
         "1,2,3,0,gfx950,broken,x,64,64,8,2",   # malformed: ignored
         "1,2,3",                                # short: ignored
     ]) + "\n", encoding="utf-8")
@@ -76,7 +76,7 @@ def test_matmul_cache_v2_round_trip_and_bad_rows(tmp_path):
     assert sorted(rows) == sorted([
         "1024,1024,1024,0,gfx950,f32_dp_64x64x64,64,64,64,8,2",
         "4096,4096,4096,1,gfx950,half_lds_256x256,256,256,64,8,1",
-        "12,13,14,2,gfx950,half_skinny_16x32,16,32,32,4,4",
+        "12,13,14,2,gfx950,half_skinny_16x64,16,64,256,8,2",
     ])
 
 
