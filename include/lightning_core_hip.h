@@ -489,6 +489,102 @@ size_t lcHipAttentionTuneCacheSize(void);
  * reference's cwd-relative candidates; CJ_RUNTIME_PROFILE_AUTOLOAD=0 skips). */
 void lcPreloadRuntimeProfileEnv(void);
 
+/* --- graph IR on hip (reference lightning_core::graph::GraphIR,
+ * include/lightning_core/core/graph.hpp; its Python class GraphIR,
+ * python/bindings/bind_graph.cpp:340-906) ------------------------------------
+ * The nine operators ("matmul", "vector_add", "matrix_sub", "matrix_div",
+ * "attention_forward", "conv2d_nchw3x3", "conv2d_nchw3x3s1p1",
+ * "qkv_pack_repeat", "relu") with the reference's schemas plus a hip column,
+ * its validation passes and reason codes, the capability-scored planner with
+ * sync boundaries and plan cache, the fusion report with cost model v1/v2,
+ * and an executor that runs every node on the GPU.  Reporting calls keep a
+ * JSON report in the graph (the report of the last call on that graph),
+ * copied out by lcGraphReport; calls on one graph are serialised.  Tensor
+ * dtype: 0 float32, 1 float64; layout: 0 contiguous, 1 strided.  No
+ * counterpart in the reference C ABI (its graph is C++ / pybind only). */
+typedef struct lcGraph lcGraph;
+
+/* GraphPlannerOptions (graph.hpp:462-499); sync_mode 0 auto, 1 always,
+ * 2 never; NULL strings mean the reference defaults
+ * ("conv,matmul,attention,attention_qkv", "auto"). */
+typedef struct lcGraphPlannerOptions {
+  lcDeviceKind preferred_device;
+  int sync_mode;
+  int trace_sync_boundary;
+  int group_by_backend_capability;
+  int separate_fallback_segments;
+  int insert_sync_on_device_change;
+  int enable_fusion_v1;
+  int enable_fusion_pass_conv;
+  int enable_fusion_pass_matmul;
+  int enable_fusion_pass_attention;
+  int enable_fusion_pass_attention_qkv;
+  const char* fusion_pass_order;
+  int enable_fusion_cost_model_v1;
+  int enable_fusion_cost_model_v2;
+  int enable_plan_cache;
+  const char* cost_profile_signature;
+  double fusion_cost_min_speedup;
+  double cost_launch_overhead_ns;
+  double cost_transfer_overhead_ns;
+  double cost_sync_boundary_ns;
+  double cost_elementwise_per_element_ns;
+  double cost_matmul_per_mac_ns;
+  double cost_conv_per_mac_ns;
+  double planner_cost_weight_compute;
+  double planner_cost_weight_boundary;
+  double planner_cost_weight_preference;
+} lcGraphPlannerOptions;
+
+/* The reference defaults with preferred_device = LC_DEVICE_HIP. */
+lcGraphPlannerOptions lcGraphPlannerOptionsDefault(void);
+lcError_t lcGraphCreate(lcGraph** out);
+lcError_t lcGraphDestroy(lcGraph* g);
+/* GraphIR::addTensorSpec (graph.hpp:620-640): every dimension > 0. */
+lcError_t lcGraphAddTensor(lcGraph* g, const int64_t* shape, size_t rank, int dtype, int layout, const char* name,
+                           int constant, size_t* out_id);
+/* GraphIR::addNode (graph.hpp:642-684): an unknown op is LC_NOT_SUPPORTED;
+ * wrong arity, tensor ids out of range or control dependencies on later
+ * nodes are LC_INVALID_VALUE.  Attributes as parallel arrays. */
+lcError_t lcGraphAddNode(lcGraph* g, const char* op, const size_t* inputs, size_t n_inputs, const size_t* outputs,
+                         size_t n_outputs, const size_t* control_deps, size_t n_control_deps, const char* name,
+                         const char* const* attr_keys, const int64_t* attr_values, size_t n_attrs);
+lcError_t lcGraphCounts(lcGraph* g, size_t* num_tensors, size_t* num_nodes);
+/* GraphIR::planCacheStats / clearPlanCache (graph.hpp:1722-1738). */
+lcError_t lcGraphPlanCacheStats(lcGraph* g, size_t* hits, size_t* misses);
+lcError_t lcGraphClearPlanCache(lcGraph* g);
+/* Copies the report of the last reporting call on g: json == NULL (or
+ * cap == 0) only sets *needed (bytes including the NUL); a smaller buffer is
+ * LC_INVALID_VALUE.  Has no other effect. */
+lcError_t lcGraphReport(lcGraph* g, char* json, size_t cap, size_t* needed);
+/* Report {"tensors": [...], "nodes": [...]} (bind_graph.cpp:408-421). */
+lcError_t lcGraphDescribe(lcGraph* g);
+/* graph_registry_schemas (bind_graph.cpp:323-330) as a JSON list. */
+lcError_t lcGraphRegistry(char* json, size_t cap, size_t* needed);
+/* validateWithReport (graph.hpp:690-1062): report {"ok", "status", "issues"},
+ * written whatever the outcome; returns the validation status. */
+lcError_t lcGraphValidate(lcGraph* g);
+/* planForDevice (graph.hpp:1064-1079): report = the plan steps. */
+lcError_t lcGraphPlanForDevice(lcGraph* g, lcDeviceKind preferred_device);
+/* plan_groups (bind_graph.cpp:440-508): {"groups", "steps", "summary"}. */
+lcError_t lcGraphPlanGroups(lcGraph* g, const lcGraphPlannerOptions* options);
+/* planSummary (graph.hpp:1325-1361): {"summary", "groups", "steps"}. */
+lcError_t lcGraphPlanSummary(lcGraph* g, const lcGraphPlannerOptions* options);
+/* fusionReport (graph.hpp:1392-1707): the fusion decisions as a list. */
+lcError_t lcGraphFusionReport(lcGraph* g, const lcGraphPlannerOptions* options);
+/* executeF32 (graph.hpp:1364-1372) on hip: feeds (host fp32, feed_sizes
+ * elements each, equal to the tensor's element count) are uploaded once;
+ * every node runs on the GPU in plan order with the reference's fusion walk
+ * (graph.hpp:3586-3840); the requested tensors are copied to `outputs` after
+ * one sync.  Report {"groups", "steps", "summary"}.  A plan that puts any
+ * node on another device (preferred_device "cpu", float64 tensors) is
+ * LC_NOT_SUPPORTED naming the node, before any launch: this backend has no
+ * CPU compute path.  A tensor that is neither fed nor produced, when read or
+ * requested, is LC_INVALID_VALUE. */
+lcError_t lcGraphExecuteF32(lcGraph* g, const lcGraphPlannerOptions* options, const size_t* feed_ids,
+                            const float* const* feeds, const size_t* feed_sizes, size_t n_feeds,
+                            const size_t* output_ids, float* const* outputs, size_t n_outputs);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,6 +71,13 @@ hipError_t im2colF32(const float* x, float* cols, int batch, int C, int H, int W
 // Fills dst with the first `total` floats of the infinite repetition of src[0:n].
 hipError_t repeatFillF32(const float* src, size_t n, float* dst, size_t total, hipStream_t stream);
 
+// out[i] = a[i] (op) b[i] (b unused by kRelu); each element is read before it
+// is written, so out may alias a or b.  kAddRelu also stores the sum before
+// the ReLU to `sum` when that is not null.
+enum class ElementwiseOp { kAdd = 0, kSub = 1, kDiv = 2, kRelu = 3, kAddRelu = 4 };
+hipError_t elementwiseF32(ElementwiseOp op, const float* a, const float* b, float* out, float* sum, size_t n,
+                          hipStream_t stream);
+
 // x = relu?(x*scale + bias), in place (the attention output postprocess,
 // reference src/attention.cpp:41-60).
 hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu, hipStream_t stream);

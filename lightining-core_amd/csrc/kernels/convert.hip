@@ -127,6 +127,31 @@ __global__ __launch_bounds__(256) void repeat_fill_kernel(const float* __restric
   }
 }
 
+// out = a (op) b elementwise: 0 add, 1 sub, 2 div, 3 relu(a), 4 relu(a + b)
+// (and a + b to `sum` when it is not null).
+__global__ __launch_bounds__(256) void elementwise_f32_kernel(int op, const float* a, const float* b, float* out,
+                                                              float* sum, size_t n) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * 256) {
+    const float x = a[i];
+    float v;
+    switch (op) {
+      case 0: v = x + b[i]; break;
+      case 1: v = x - b[i]; break;
+      case 2: v = x / b[i]; break;
+      case 3: v = x < 0.0f ? 0.0f : x; break;
+      default: {
+        const float y = x + b[i];
+        if (sum != nullptr) {
+          sum[i] = y;
+        }
+        v = y < 0.0f ? 0.0f : y;
+      }
+    }
+    out[i] = v;
+  }
+}
+
 __global__ __launch_bounds__(256) void postprocess_kernel(float* __restrict__ x, size_t n, float scale, float bias,
                                                           int relu) {
   for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
@@ -219,6 +244,16 @@ hipError_t repeatFillF32(const float* src, size_t n, float* dst, size_t total, h
 }  // namespace lchip::kern
 
 namespace lchip::kern {
+
+hipError_t elementwiseF32(ElementwiseOp op, const float* a, const float* b, float* out, float* sum, size_t n,
+                          hipStream_t stream) {
+  if (n == 0) {
+    return hipSuccess;
+  }
+  hipLaunchKernelGGL(elementwise_f32_kernel, dim3(grid_for(n)), dim3(256), 0, stream, static_cast<int>(op), a, b,
+                     out, sum, n);
+  return hipGetLastError();
+}
 
 hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu, hipStream_t stream) {
   if (n == 0) {

@@ -15,5 +15,9 @@ Everything calls the C ABI in include/lightning_core_hip.h through ctypes;
 there is no Python or CPU implementation of any kernel here.
 """
 from ._core import *  # noqa: F401,F403
-from ._core import __all__  # noqa: F401
+from ._core import __all__ as _core_all
+from ._graph import *  # noqa: F401,F403
+from ._graph import __all__ as _graph_all
 from . import api  # noqa: F401
+
+__all__ = list(_core_all) + list(_graph_all)

@@ -99,6 +99,23 @@ class VitBlockConfig(ctypes.Structure):
                 ("patch", c_size), ("embed", c_size), ("heads", c_size), ("compute_dtype", c_int)]
 
 
+class GraphPlannerOptions(ctypes.Structure):
+    """lcGraphPlannerOptions."""
+    _fields_ = [("preferred_device", c_int), ("sync_mode", c_int), ("trace_sync_boundary", c_int),
+                ("group_by_backend_capability", c_int), ("separate_fallback_segments", c_int),
+                ("insert_sync_on_device_change", c_int), ("enable_fusion_v1", c_int),
+                ("enable_fusion_pass_conv", c_int), ("enable_fusion_pass_matmul", c_int),
+                ("enable_fusion_pass_attention", c_int), ("enable_fusion_pass_attention_qkv", c_int),
+                ("fusion_pass_order", c_char_p), ("enable_fusion_cost_model_v1", c_int),
+                ("enable_fusion_cost_model_v2", c_int), ("enable_plan_cache", c_int),
+                ("cost_profile_signature", c_char_p), ("fusion_cost_min_speedup", ctypes.c_double),
+                ("cost_launch_overhead_ns", ctypes.c_double), ("cost_transfer_overhead_ns", ctypes.c_double),
+                ("cost_sync_boundary_ns", ctypes.c_double), ("cost_elementwise_per_element_ns", ctypes.c_double),
+                ("cost_matmul_per_mac_ns", ctypes.c_double), ("cost_conv_per_mac_ns", ctypes.c_double),
+                ("planner_cost_weight_compute", ctypes.c_double), ("planner_cost_weight_boundary", ctypes.c_double),
+                ("planner_cost_weight_preference", ctypes.c_double)]
+
+
 class HipDeviceInfo(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 128), ("gcn_arch", ctypes.c_char * 64), ("compute_units", c_int),
                 ("max_clock_khz", c_int), ("total_memory_bytes", c_size), ("l2_cache_bytes", c_size)]
@@ -204,6 +221,26 @@ SIGNATURES = {
     "lcHipAttentionResetTuning": (_E, []),
     "lcHipAttentionTuneCacheSize": (c_size, []),
     "lcPreloadRuntimeProfileEnv": (None, []),
+    # graph IR on hip
+    "lcGraphPlannerOptionsDefault": (GraphPlannerOptions, []),
+    "lcGraphCreate": (_E, [P(c_void_p)]),
+    "lcGraphDestroy": (_E, [c_void_p]),
+    "lcGraphAddTensor": (_E, [c_void_p, P(ctypes.c_int64), c_size, c_int, c_int, c_char_p, c_int, P(c_size)]),
+    "lcGraphAddNode": (_E, [c_void_p, c_char_p, P(c_size), c_size, P(c_size), c_size, P(c_size), c_size, c_char_p,
+                            P(c_char_p), P(ctypes.c_int64), c_size]),
+    "lcGraphCounts": (_E, [c_void_p, P(c_size), P(c_size)]),
+    "lcGraphPlanCacheStats": (_E, [c_void_p, P(c_size), P(c_size)]),
+    "lcGraphClearPlanCache": (_E, [c_void_p]),
+    "lcGraphReport": (_E, [c_void_p, ctypes.c_char_p, c_size, P(c_size)]),
+    "lcGraphDescribe": (_E, [c_void_p]),
+    "lcGraphRegistry": (_E, [ctypes.c_char_p, c_size, P(c_size)]),
+    "lcGraphValidate": (_E, [c_void_p]),
+    "lcGraphPlanForDevice": (_E, [c_void_p, c_int]),
+    "lcGraphPlanGroups": (_E, [c_void_p, P(GraphPlannerOptions)]),
+    "lcGraphPlanSummary": (_E, [c_void_p, P(GraphPlannerOptions)]),
+    "lcGraphFusionReport": (_E, [c_void_p, P(GraphPlannerOptions)]),
+    "lcGraphExecuteF32": (_E, [c_void_p, P(GraphPlannerOptions), P(c_size), P(c_void_p), P(c_size), c_size,
+                               P(c_size), P(c_void_p), c_size]),
 }
 
 _lib = None
