@@ -1442,7 +1442,7 @@ struct RingRowMajor {
 
 // Implicit im2col of a patch-embedding convolution (kernel = stride = P, no
 // padding) over x [B, C, H, W]: row = b*T + ty*gw + tx, k = (c*P + ky)*P + kx.
-// With P dividing 64 and 64 dividing P*P a 64-wide stage is 64/P kernel rows
+// With P dividing BK and BK dividing P*P a BK-wide stage is BK/P kernel rows
 // of one channel: k0 fixes (c, first ky) for every lane (the stage base) and
 // the lane adds its patch origin plus kk / P rows and kk % P columns.
 struct RingPatch {
@@ -1464,22 +1464,32 @@ struct RingPatch {
   }
 };
 
-template <typename T, int BM, int BN, int WM, int WN, int NS, typename ASrc, typename Epi>
+// BK = 64 (128-byte LDS rows, chunk c of row r at c ^ ((r >> 1) & 7)) or
+// BK = 128 (256-byte rows, chunk c at c ^ (r & 15)): each 1 KB copy then
+// fills 8 or 4 rows.  The deeper stage halves the per-stage waits and
+// barriers: in the ViT block (K = 768, 128x64 tiles, three 48 KiB stages)
+// the patch GEMM went 9.5 -> 8.8 us and the output projection 7.8 -> 7.3 us
+// (kernel trace); the k order, and so the result, is unchanged.
+template <typename T, int BM, int BN, int WM, int WN, int NS, typename ASrc, typename Epi, int BK = 64>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, const uint16_t* __restrict__ Bt,
                                                                        int M, int N, int K, int ldb, int tiles_n,
                                                                        Epi epi) {
-  constexpr int BK = 64;
+  static_assert(BK == 64 || BK == 128, "stage depth");
   constexpr int NW = WM * WN;
   constexpr int TM = BM / WM / 32;
   constexpr int TN = BN / WN / 32;
   constexpr int ROWB = BK * 2;                 // bytes per LDS row
+  constexpr int RPI = 1024 / ROWB;             // rows per 1 KB copy
+  constexpr int CPR = ROWB / 16;               // 16-byte chunks per row
   constexpr int STAGE = (BM + BN) * BK;        // elements per stage
-  constexpr int A_INS = BM / 8;                // 1 KB copies of A per stage
-  constexpr int LPW = (BM + BN) / 8 / NW;      // copies per wave per stage
+  constexpr int A_INS = BM / RPI;              // 1 KB copies of A per stage
+  constexpr int LPW = (BM + BN) / RPI / NW;    // copies per wave per stage
   constexpr int A_LPW = A_INS / NW;            // ... of which A
-  static_assert(TM >= 1 && TN >= 1 && A_INS % NW == 0 && (BN / 8) % NW == 0, "tile / wave split");
+  static_assert(TM >= 1 && TN >= 1 && A_INS % NW == 0 && (BN / RPI) % NW == 0, "tile / wave split");
   static_assert(NS >= 2 && NS <= 5 && NS * STAGE * 2 <= 160 * 1024, "LDS ring");
+  static_assert(3 * LPW < 64, "vmcnt immediate");
   __shared__ __attribute__((aligned(16))) uint16_t smem[NS * STAGE];
+  auto swz = [](int r) { return BK == 64 ? ((r >> 1) & 7) : (r & 15); };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -1502,15 +1512,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, 
   const int bm = (first_m + in_group % gm) * BM;
   const int bn = (in_group / gm) * BN;
 
-  // Copy j of this wave is instruction i = wave + NW*j: A rows 8i..8i+7 for
-  // j < A_LPW, else B rows 8(i - A_INS)..; lane l -> row + l/8, physical
-  // chunk l%8, logical chunk (l%8) ^ ((row >> 1) & 7).
+  // Copy j of this wave is instruction i = wave + NW*j: A rows RPI*i ..
+  // RPI*i + RPI-1 for j < A_LPW, else B rows RPI*(i - A_INS)..; lane l ->
+  // row + l/CPR, physical chunk l%CPR, logical chunk (l%CPR) ^ swz(row).
   uint32_t off[LPW];
 #pragma unroll
   for (int j = 0; j < LPW; ++j) {
     const int ins = wave + NW * j;
-    const int r = 8 * (j < A_LPW ? ins : ins - A_INS) + (lane >> 3);
-    const int kk = ((lane & 7) ^ ((r >> 1) & 7)) * 8;
+    const int r = RPI * (j < A_LPW ? ins : ins - A_INS) + lane / CPR;
+    const int kk = ((lane % CPR) ^ swz(r)) * 8;
     if (j < A_LPW) {
       off[j] = asrc.lane_offset(bm, min(bm + r, M - 1), kk);
     } else {
@@ -1524,7 +1534,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, 
     const uint16_t* a_base = asrc.stage_base(bm, k0);
 #pragma unroll
     for (int j = 0; j < LPW; ++j) {
-      const uint32_t dst = lds0 + 2u * static_cast<uint32_t>(buf * STAGE + (wave_s + NW * j) * 8 * BK);
+      const uint32_t dst = lds0 + 2u * static_cast<uint32_t>(buf * STAGE + (wave_s + NW * j) * RPI * BK);
       load_lds16_sbase(off[j], j < A_LPW ? a_base : b_tile + k0, dst);
     }
   };
@@ -1532,8 +1542,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, 
   const int lrow = lane & 31;
   const int lhalf = lane >> 5;
   auto frag = [&](const uint16_t* base, int row, int c) -> u32x4 {
-    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + row * ROWB +
-                                           ((c ^ ((row >> 1) & 7)) << 4));
+    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(base) + row * ROWB + ((c ^ swz(row)) << 4));
   };
   floatx16 acc[TM][TN];
 #pragma unroll
@@ -2071,13 +2080,16 @@ static hipError_t launch_gemm_half(LoadA load_a, const uint16_t* Bt, int M, int 
   return launch_gemm_half_tile<T>(pick_half_tile(M, N, false), load_a, Bt, M, N, K, ldb, epi, stream);
 }
 
-template <typename T, int BM, int BN, int WM, int WN, int NS, typename ASrc, typename Epi>
+template <typename T, int BM, int BN, int WM, int WN, int NS, int BK = 64, typename ASrc, typename Epi>
 static hipError_t launch_gemm_ring(ASrc asrc, const uint16_t* Bt, int M, int N, int K, int ldb, Epi epi,
                                    hipStream_t stream) {
+  if (K % BK != 0) {
+    return hipErrorInvalidValue;
+  }
   const int tiles_n = (N + BN - 1) / BN;
   const dim3 grid(((M + BM - 1) / BM) * tiles_n);
-  hipLaunchKernelGGL((gemm_half_ring_kernel<T, BM, BN, WM, WN, NS, ASrc, Epi>), grid, dim3(WM * WN * 64), 0, stream,
-                     asrc, Bt, M, N, K, ldb, tiles_n, epi);
+  hipLaunchKernelGGL((gemm_half_ring_kernel<T, BM, BN, WM, WN, NS, ASrc, Epi, BK>), grid, dim3(WM * WN * 64), 0,
+                     stream, asrc, Bt, M, N, K, ldb, tiles_n, epi);
   return hipGetLastError();
 }
 
@@ -2085,6 +2097,12 @@ static hipError_t launch_gemm_ring(ASrc asrc, const uint16_t* Bt, int M, int N, 
 inline bool vit_ring_enabled() {
   const char* env = getenv("CJ_HIP_VIT_RING");
   return env == nullptr || std::string(env) != "0";
+}
+
+// 128-deep ring stages where K allows them, unless CJ_HIP_VIT_RING_BK is 64.
+inline bool vit_ring_bk128(long long K) {
+  const char* env = getenv("CJ_HIP_VIT_RING_BK");
+  return K % 128 == 0 && (env == nullptr || std::string(env) != "64");
 }
 
 // Its copies use 32-bit byte offsets from a stage base and 16-byte alignment.
@@ -2309,7 +2327,14 @@ hipError_t patchEmbedGemm(const uint16_t* x, const uint16_t* Wt, uint16_t* token
       static_cast<long long>(B) * C * H * W * 2 < (1LL << 31) && ring_fits(128, K)) {
     // 128x64 tiles (8 waves of 32x32): 156 workgroups at B = 8, 43 flop per
     // copied byte; measured faster than 64x64 (300 workgroups, 32 flop/B).
+    // A 128-deep stage is 128/P kernel rows of one channel (P | 128, 128 | P*P).
     const RingPatch ra{x, C, H, W, P, T_, gw};
+    if (P >= 16 && vit_ring_bk128(K)) {
+      if (t == Half::kBF16) {
+        return launch_gemm_ring<BF16, 128, 64, 4, 2, 3, 128>(ra, Wt, M, E, K, K, EpiHalf<BF16>{tokens, E, 1}, stream);
+      }
+      return launch_gemm_ring<F16, 128, 64, 4, 2, 3, 128>(ra, Wt, M, E, K, K, EpiHalf<F16>{tokens, E, 1}, stream);
+    }
     if (t == Half::kBF16) {
       return launch_gemm_ring<BF16, 128, 64, 4, 2, 4>(ra, Wt, M, E, K, K, EpiHalf<BF16>{tokens, E, 1}, stream);
     }
@@ -2333,6 +2358,9 @@ hipError_t qkvProjectGemm(const uint16_t* tokens, const uint16_t* Wqkv_t, uint16
   if (vit_ring_enabled() && ring_fits(128, E) && T_ % 4 == 0) {
     // 128x128 tiles (8 waves): 234 workgroups for the B = 8 block, one per
     // CU; measured faster than 64x64 tiles (900 workgroups).
+    // 64-deep stages here: a 128-deep stage of this tile is 64 KiB, so only
+    // two fit and one stage is in flight; in the block, where the tokens come
+    // cold from the patch GEMM, that measured 13.2 against 12.9 us.
     const RingRowMajor ra{tokens, E};
     if (t == Half::kBF16) {
       return launch_gemm_ring<BF16, 128, 128, 2, 4, 4>(ra, Wqkv_t, M, 3 * E, E, E,
@@ -2355,6 +2383,12 @@ hipError_t outProjectGemm(const uint16_t* attn, const uint16_t* Wo_t, float* out
   }
   if (vit_ring_enabled() && ring_fits(128, E)) {
     const RingRowMajor ra{attn, E};
+    if (vit_ring_bk128(E)) {
+      if (t == Half::kBF16) {
+        return launch_gemm_ring<BF16, 128, 64, 4, 2, 3, 128>(ra, Wo_t, M, E, E, E, EpiF32{out, E}, stream);
+      }
+      return launch_gemm_ring<F16, 128, 64, 4, 2, 3, 128>(ra, Wo_t, M, E, E, E, EpiF32{out, E}, stream);
+    }
     if (t == Half::kBF16) {
       return launch_gemm_ring<BF16, 128, 64, 4, 2, 4>(ra, Wo_t, M, E, E, E, EpiF32{out, E}, stream);
     }

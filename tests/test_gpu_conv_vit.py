@@ -184,6 +184,20 @@ def test_vit_block_ring_off_matches(lc, monkeypatch):
     assert np.abs(ring - plain).max() <= 2e-2 * np.abs(plain).max()
 
 
+@pytest.mark.parametrize("p,e", [(16, 128), (32, 256), (8, 128)])
+def test_vit_block_ring_stage_depth_bitwise(lc, monkeypatch, p, e):
+    # The patch and output GEMMs take 128-deep ring stages when K allows
+    # (CJ_HIP_VIT_RING_BK=64 forces 64): same k order, so the same bits.  P = 8
+    # keeps 64-deep stages for the patch GEMM (a 128-deep stage would span
+    # two channels) and checks that path too.
+    bn, c, img, heads = 2, 3, 64, 2
+    x, w_conv, w_qkv, w_o = _vit_inputs(bn, c, img, p, e)
+    deep = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype="f16")
+    monkeypatch.setenv("CJ_HIP_VIT_RING_BK", "64")
+    shallow = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype="f16")
+    np.testing.assert_array_equal(deep, shallow)
+
+
 def test_vit_block_config4(lc, oracle):
     bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12
     note("[case] config 4 ViT block")
