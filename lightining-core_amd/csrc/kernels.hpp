@@ -89,6 +89,15 @@ hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu,
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D,
                         bool causal, float post_scale, float post_bias, int post_relu, float* stats,
                         hipStream_t stream, int splits = 0);
+// The `splits` value that selects the 16-query fp32 forward kernel
+// (attn_fwd_f32_q16_kernel: 16 waves of 16-key tiles per 16 queries), for
+// problems too small to fill the GPU.  Needs D <= 64, D % 4 == 0 and 16-byte
+// aligned q / k / v; otherwise attentionF32 takes its heuristic split.
+constexpr int kAttnF32Q16 = 16;
+// attentionF32's choice for splits = 0: the 16-query kernel while its grid is
+// at most one workgroup per CU (bh * S/16 <= 256, S <= 1024, D <= 64,
+// D % 4 == 0), else the split heuristic below.
+int attentionF32DefaultSplits(int bh, int S, int D);
 // Key splits (waves per 32 queries) attentionF32 / attentionDvUpdateF32 use:
 // `requested` (1, 2, 4 or 8) limited to what the head dim allows, or the
 // heuristic when requested is 0.

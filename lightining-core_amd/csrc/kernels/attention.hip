@@ -517,6 +517,223 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
 }
 
 // ---------------------------------------------------------------------------
+// fp32 attention for problems too small to fill the GPU (one head, S of a few
+// hundred): 16 queries per workgroup and KS = 16 waves, wave w taking the
+// 16-key tiles w, w + KS, ... with v_mfma_f32_16x16x4_f32.  At S = 256 that
+// is 16 workgroups x 16 waves, each wave one 16 x 16 score tile (16 + 16
+// MFMAs of 32 cycles) where attn_fwd_f32_kernel<2, 8> gives each of its 64
+// waves a 32 x 32 tile (64 MFMAs of 64 cycles).  D <= 64, D % 4 == 0 and
+// 16-byte aligned K / V rows (float4 loads); the KS states merge through LDS
+// as in attn_fwd_f32_kernel.
+//
+// Scores are S^T = K . Q^T per tile: lane l holds keys 4g + i (g = l / 16,
+// i = 0..3) of query c = l % 16.  The QK^T reduction over d gives lane group
+// g the d range [g DP/4, (g+1) DP/4).  For O^T += V^T . P^T, k-step s takes
+// keys {4g + s}, so each lane feeds its own probability st[s] as the B operand
+// and reads V row 4g + s; output row d = 16 dt + 4g + i, column c.
+// ---------------------------------------------------------------------------
+template <int DQ, int KS>
+__global__ __launch_bounds__(64 * KS) void attn_fwd_f32_q16_kernel(const float* __restrict__ q,
+                                                                   const float* __restrict__ k,
+                                                                   const float* __restrict__ v,
+                                                                   float* __restrict__ out, float* __restrict__ stats,
+                                                                   int S, int D, int causal, float scale,
+                                                                   float post_scale, float post_bias, int post_relu) {
+  constexpr int DP = 16 * DQ;
+  constexpr int QS = DP + 4;             // Q / K row stride (16-byte aligned rows)
+  constexpr int KVF = 16 * QS + 16 * DP; // floats of one wave's K + V tile
+  constexpr int PS = DP + 1;             // parked O row stride
+  static_assert(DQ >= 1 && DQ <= 4 && 32 + 16 * PS <= KVF, "tile");
+  __shared__ __attribute__((aligned(16))) float Qs[16 * QS];
+  __shared__ __attribute__((aligned(16))) float kv[KS][KVF];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  float* Ks = &kv[wave][0];
+  float* Vs = &kv[wave][16 * QS];
+  const int nqb = (S + 15) / 16;
+  const int q0 = (nqb - 1 - static_cast<int>(blockIdx.x)) * 16;  // heaviest (causal) blocks first
+  const size_t head = static_cast<size_t>(blockIdx.y) * S * D;
+  const int qi = q0 + c;
+  const int kend = causal ? min(S, q0 + 16) : S;
+  const int jfirst = wave * 16;
+  constexpr int jstep = 16 * KS;
+
+  // One tile of K and V is 16 rows x DP/4 float4: DQ chunks per lane each.
+  float4 kr[DQ], vr[DQ];
+  auto fetch = [&](int j0) {
+#pragma unroll
+    for (int t = 0; t < DQ; ++t) {
+      const int idx = t * 64 + lane;  // row idx / (DP/4), column 4 (idx % (DP/4))
+      const int r = idx / (DP / 4);
+      const int cc = (idx - r * (DP / 4)) * 4;
+      const bool ok = j0 + r < S && cc < D;
+      const size_t off = head + static_cast<size_t>(j0 + r) * D + cc;
+      kr[t] = ok ? *reinterpret_cast<const float4*>(k + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      vr[t] = ok ? *reinterpret_cast<const float4*>(v + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  };
+  if (jfirst < kend) {
+    fetch(jfirst);  // out before the Q loads, so the latencies overlap
+  }
+  for (int idx = threadIdx.x; idx < 16 * (DP / 4); idx += 64 * KS) {
+    const int r = idx / (DP / 4);
+    const int cc = (idx - r * (DP / 4)) * 4;
+    const bool ok = q0 + r < S && cc < D;
+    *reinterpret_cast<float4*>(&Qs[r * QS + cc]) =
+        ok ? *reinterpret_cast<const float4*>(q + head + static_cast<size_t>(q0 + r) * D + cc)
+           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  __syncthreads();
+
+  floatx4 o[DQ];
+#pragma unroll
+  for (int t = 0; t < DQ; ++t) {
+    o[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  float m_run = kMaskValue;
+  float l_run = 0.0f;
+  for (int j0 = jfirst; j0 < kend; j0 += jstep) {
+#pragma unroll
+    for (int t = 0; t < DQ; ++t) {
+      const int idx = t * 64 + lane;
+      const int r = idx / (DP / 4);
+      const int cc = (idx - r * (DP / 4)) * 4;
+      *reinterpret_cast<float4*>(&Ks[r * QS + cc]) = kr[t];
+      *reinterpret_cast<float4*>(&Vs[r * DP + cc]) = vr[t];
+    }
+    if (j0 + jstep < kend) {
+      fetch(j0 + jstep);
+    }
+    __builtin_amdgcn_wave_barrier();  // only this wave reads its K / V tile
+
+    floatx4 st = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    {
+      const float* krow = &Ks[c * QS + g * (DP / 4)];
+      const float* qrow = &Qs[c * QS + g * (DP / 4)];
+#pragma unroll
+      for (int t4 = 0; t4 < DP / 4; t4 += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(krow + t4);
+        const float4 b4 = *reinterpret_cast<const float4*>(qrow + t4);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, st, 0, 0, 0);
+      }
+    }
+    float mt = kMaskValue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = j0 + 4 * g + i;
+      // (q.k) * scale as the reference, then to the log2 domain
+      float x = (st[i] * scale) * kLog2e;
+      if (key >= S || (causal && key > qi)) {
+        x = kMaskValue;
+      }
+      st[i] = x;
+      mt = fmaxf(mt, x);
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16));
+    mt = fmaxf(mt, __shfl_xor(mt, 32));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = exp2f(m_run - m_new);
+    float ls = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float p = exp2f(st[i] - m_new);
+      st[i] = p;
+      ls += p;
+    }
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+#pragma unroll
+    for (int t = 0; t < DQ; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o[t][i] *= alpha;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int t = 0; t < DQ; ++t) {
+        const float a = Vs[(4 * g + s) * DP + t * 16 + c];
+        o[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, st[s], o[t], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the next tile overwrites K / V of this one
+  }
+  l_run += __shfl_xor(l_run, 16);
+  l_run += __shfl_xor(l_run, 32);
+
+  // Park each wave's state in its K / V region: m, l (16 each), then O as
+  // [query][d] (row stride DP + 1); a wave that saw no tile parks m = -1e30,
+  // l = 0, O = 0.
+  float* mine = &kv[wave][0];
+  if (lane < 16) {
+    mine[lane] = m_run;
+    mine[16 + lane] = l_run;
+  }
+#pragma unroll
+  for (int t = 0; t < DQ; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mine[32 + c * PS + t * 16 + 4 * g + i] = o[t][i];
+    }
+  }
+  __syncthreads();
+  // Thread (query ql, slot) merges output columns d = slot, slot + 4 KS, ...
+  const int ql = threadIdx.x & 15;
+  const int slot = threadIdx.x >> 4;
+  float m_all = kMaskValue;
+#pragma unroll
+  for (int w = 0; w < KS; ++w) {
+    m_all = fmaxf(m_all, kv[w][ql]);
+  }
+  float f[KS];
+  float l_all = 0.0f;
+#pragma unroll
+  for (int w = 0; w < KS; ++w) {
+    f[w] = exp2f(kv[w][ql] - m_all);
+    l_all += f[w] * kv[w][16 + ql];
+  }
+  const float inv = 1.0f / l_all;
+  // Row statistics for a pass that recomputes P (the train step's dV):
+  // p = exp2(x - m) / l with x = (q.k) * scale * log2(e).
+  if (stats != nullptr && threadIdx.x < 16 && q0 + ql < S) {
+    stats[(static_cast<size_t>(blockIdx.y) * S + q0 + ql) * 2] = m_all;
+    stats[(static_cast<size_t>(blockIdx.y) * S + q0 + ql) * 2 + 1] = l_all;
+  }
+  constexpr int TS = DP + 1;
+  float* tile = Qs;  // 16 x (DP + 1) <= 16 x QS floats; every wave is past its QK^T
+  for (int d = slot; d < D; d += 4 * KS) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < KS; ++w) {
+      acc += f[w] * kv[w][32 + ql * PS + d];
+    }
+    float val = acc * inv;
+    if (post_scale != 1.0f || post_bias != 0.0f || post_relu) {
+      val = val * post_scale + post_bias;
+      if (post_relu && val < 0.0f) {
+        val = 0.0f;
+      }
+    }
+    tile[ql * TS + d] = val;
+  }
+  __syncthreads();
+  // Rows q0 .. q0 + rows - 1 are one contiguous range of out.
+  const int rows = min(16, S - q0);
+  float* dst = out + head + static_cast<size_t>(q0) * D;
+  for (int r = wave; r < rows; r += KS) {
+    if (lane < D) {
+      dst[r * D + lane] = tile[r * TS + lane];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Train step backward (fp32): dV = P^T . dO with dO = 2 (out - target) / (S*D),
 // then V -= lr * dV in place (the reference's attentionTrainStepCpu,
 // src/attention_cpu.cpp:114-163).  P is not stored: the forward left each
@@ -1074,9 +1291,24 @@ namespace lchip::kern {
 
 using namespace lchip::k;
 
+bool attentionF32Q16Fits(int D, const float* k, const float* v, const float* q) {
+  return D <= 64 && D % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(v) % 16 == 0 && reinterpret_cast<uintptr_t>(q) % 16 == 0;
+}
+
+int attentionF32DefaultSplits(int bh, int S, int D) {
+  if (D <= 64 && D % 4 == 0 && bh * ((S + 15) / 16) <= 256 && S <= 1024) {
+    return kAttnF32Q16;
+  }
+  return attentionF32Splits(bh, S, D, 0);
+}
+
 int attentionF32Splits(int bh, int S, int D, int requested) {
   const int nqb = (S + 31) / 32;
   const int dt = (D + 31) / 32;
+  if (requested == kAttnF32Q16 && D <= 64 && D % 4 == 0) {
+    return kAttnF32Q16;
+  }
   // Per-wave K + V tiles must fit the 160 KB of LDS: up to 8 splits at
   // DT <= 2 (140 KB), 2 at DT <= 4, 1 beyond (the launch switches below).
   const int cap = dt <= 2 ? 8 : (dt <= 4 ? 2 : 1);
@@ -1103,11 +1335,38 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
     return hipErrorInvalidValue;
   }
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
+  const int cz = causal ? 1 : 0;
+  // The 16-query kernel when asked for, and by default while its grid is at
+  // most one workgroup per CU (bh * S/16 <= 256, S <= 1024): measured at one
+  // head, S = 128 ... 1024, D = 32 / 64, 17-38% faster than the best split of
+  // the 32-query kernel.
+  const bool dflt = splits == 0 && attentionF32DefaultSplits(bh, S, D) == kAttnF32Q16;
+  if ((splits == kAttnF32Q16 || dflt) && attentionF32Q16Fits(D, k, v, q)) {
+    const dim3 grid16((S + 15) / 16, bh);
+    switch ((D + 15) / 16) {
+      case 1:
+        hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<1, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, stats, S, D,
+                           cz, scale, post_scale, post_bias, post_relu);
+        break;
+      case 2:
+        hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<2, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, stats, S, D,
+                           cz, scale, post_scale, post_bias, post_relu);
+        break;
+      case 3:
+        hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<3, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, stats, S, D,
+                           cz, scale, post_scale, post_bias, post_relu);
+        break;
+      default:
+        hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<4, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, stats, S, D,
+                           cz, scale, post_scale, post_bias, post_relu);
+        break;
+    }
+    return hipGetLastError();
+  }
   const int nqb = (S + 31) / 32;
   const dim3 grid(nqb, bh);
   const int dt = (D + 31) / 32;
-  const int cz = causal ? 1 : 0;
-  const int ks = attentionF32Splits(bh, S, D, splits);
+  const int ks = attentionF32Splits(bh, S, D, splits == kAttnF32Q16 ? 0 : splits);
   const bool vec = dt <= 2 && D % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(v) % 16 == 0;
   const AttnSrcGlobal src{q, k, v};
@@ -1212,8 +1471,9 @@ hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const 
   const int dt = (D + 31) / 32;
   const int cz = causal ? 1 : 0;
   // Query-tile splits: the same rule and LDS limits as the forward's key
-  // splits (K tile + per-wave Q / dO tiles).
-  const int ks = attentionF32Splits(bh, S, D, splits);
+  // splits (K tile + per-wave Q / dO tiles); the forward-only 16-query
+  // variant has no dV counterpart and reads as the heuristic.
+  const int ks = attentionF32Splits(bh, S, D, splits == kAttnF32Q16 ? 0 : splits);
 #define LC_DV_F32(DT_, KS_)                                                                                         \
   hipLaunchKernelGGL((attn_dv_f32_kernel<DT_, KS_>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out, target, stats, \
                      S, D, cz, scale, lr)

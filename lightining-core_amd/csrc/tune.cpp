@@ -13,8 +13,9 @@
 // nothing on gfx950; they are kept verbatim and written back so a file
 // shared with the reference keeps its rows.  gfx950 attention rows use their
 // own kinds (HF forward, HT train step), which the reference's reader skips,
-// and carry the arch; the value is the fp32 kernel's split count (1, 2, 4, 8),
-// and a row whose value is not one of those is dropped.
+// and carry the arch; the value is the fp32 kernel's split count (1, 2, 4, 8,
+// or 16 on forward rows for the 16-query kernel), and a row whose value is
+// not one of those is dropped.
 //
 // The runtime profile autoload restates src/runtime.cpp:101-168.
 #include <algorithm>
@@ -241,6 +242,7 @@ const char* kAttnColumns = "#columns,kind,seq,dim,causal,resident_hint,sync_hint
 const char* kAttnHipColumns = "#columns_hip,kind,seq,dim,causal,resident_hint,sync_hint,compute_loss(HT),arch,splits";
 
 bool validSplit(int mode) { return mode == 1 || mode == 2 || mode == 4 || mode == 8; }
+bool validSplit(char kind, int mode) { return validSplit(mode) || (kind == 'F' && mode == 16); }
 
 std::string joinCsv(const std::vector<std::string>& c) {
   std::string joined;
@@ -265,7 +267,7 @@ bool parseAttn(const std::string& path, std::map<AKey, int>* table, std::vector<
     try {
       if (c.size() == 8 && c[0] == "HF") {
         const int mode = std::stoi(c[7]);
-        if (validSplit(mode)) {
+        if (validSplit('F', mode)) {
           (*table)[AKey{'F', std::stoull(c[1]), std::stoull(c[2]), std::stoi(c[3]), std::stoi(c[4]),
                         std::stoi(c[5]), 0, c[6]}] = mode;
         }
@@ -380,7 +382,7 @@ bool attnTuneLookup(const AttnTuneKey& key, int* mode) {
 }
 
 void attnTuneRecord(const AttnTuneKey& key, int mode) {
-  if (!validSplit(mode)) {
+  if (!validSplit(key.kind, mode)) {
     return;
   }
   AttnCache& c = at();

@@ -187,10 +187,14 @@ def test_w4_gemm_matches_lds_bitwise(lc, tmp_path, dtype):
         assert by_name["half_w4d_256x256"] == by_name["half_lds_256x256"], shape
 
 
-@pytest.mark.parametrize("s,d,causal", [(256, 64, False), (200, 48, True), (130, 96, False)])
+@pytest.mark.parametrize("s,d,causal", [(256, 64, False), (200, 48, True), (130, 96, False), (256, 64, True),
+                                        (1000, 64, False), (33, 20, True), (17, 8, False)])
 def test_forced_attention_splits(lc, oracle, tmp_path, s, d, causal):
+    # 16 selects the 16-query kernel where D <= 64 and D % 4 == 0 (and the
+    # heuristic split elsewhere, e.g. D = 96); S = 1000 gives its waves four
+    # key tiles each (the register prefetch path), S = 17 / 33 ragged blocks.
     caches = []
-    for ks in (1, 2, 4, 8):
+    for ks in (1, 2, 4, 8, 16):
         cache = tmp_path / f"attn_{ks}.csv"
         cache.write_text("#lc_tune_cache,attention,2\n" + f"HF,{s},{d},{int(causal)},0,0,gfx950,{ks}\n"
                          + f"HF,{s},{d},{int(causal)},0,1,gfx950,{ks}\n")
@@ -210,7 +214,7 @@ def test_forced_attention_splits(lc, oracle, tmp_path, s, d, causal):
     q, k, v = (synth.normal((s, d), stream=60 + i) for i in range(3))
     ref = np.asarray(oracle.attention(q, k, v, causal)).ravel()
     outs = [l for l in out.splitlines() if l.startswith("OUT")]
-    assert len(outs) == 4
+    assert len(outs) == 5
     for line in outs:
         _, ks, payload = line.split(" ", 2)
         got = np.asarray(json.loads(payload), np.float32)
