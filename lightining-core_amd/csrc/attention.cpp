@@ -140,7 +140,7 @@ int pickSplits(const std::vector<int>& cands, const std::vector<float>& ms, int 
 
 // Split counts worth timing for one head: the valid ones (LDS limits) up to
 // the number of 32-key tiles.
-std::vector<int> splitCandidates(int S, int D, bool forward) {
+std::vector<int> splitCandidates(int S, int D) {
   const int tiles = (S + 31) / 32;
   std::vector<int> c;
   for (int ks = 1; ks <= 8; ks *= 2) {
@@ -148,9 +148,9 @@ std::vector<int> splitCandidates(int S, int D, bool forward) {
       c.push_back(ks);
     }
   }
-  // The 16-query forward kernel (D <= 64, D % 4 == 0; session buffers are
-  // 16-byte aligned) for one head of a few hundred keys or fewer.
-  if (forward && S <= 1024 && kern::attentionF32Splits(1, S, D, kern::kAttnF32Q16) == kern::kAttnF32Q16) {
+  // The 16-query forward / 16-key dV kernels (D <= 64, D % 4 == 0; session
+  // buffers are 16-byte aligned) for one head of a thousand keys or fewer.
+  if (S <= 1024 && kern::attentionF32Splits(1, S, D, kern::kAttnF32Q16) == kern::kAttnF32Q16) {
     c.push_back(kern::kAttnF32Q16);
   }
   return c;
@@ -175,7 +175,7 @@ Status forwardSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, co
   const int S = static_cast<int>(sh.seq_len);
   const int D = static_cast<int>(sh.head_dim);
   int best = kern::attentionF32DefaultSplits(1, S, D);
-  const std::vector<int> cands = splitCandidates(S, D, true);
+  const std::vector<int> cands = splitCandidates(S, D);
   if (cands.size() > 1 && autotuneEnabled("CJ_ATTN_AUTOTUNE")) {
     std::vector<float> ms;
     LC_TRY(timeCandidates(
@@ -212,8 +212,8 @@ Status trainSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, cons
   }
   const int S = static_cast<int>(sh.seq_len);
   const int D = static_cast<int>(sh.head_dim);
-  int best = kern::attentionF32Splits(1, S, D, 0);
-  const std::vector<int> cands = splitCandidates(S, D, false);
+  int best = kern::attentionF32DefaultSplits(1, S, D);
+  const std::vector<int> cands = splitCandidates(S, D);
   if (cands.size() > 1 && autotuneEnabled("CJ_ATTN_AUTOTUNE")) {
     const std::size_t bytes = sh.elems() * sizeof(float);
     LC_TRY(res.v_scratch.ensure(bytes));

@@ -905,6 +905,154 @@ __global__ __launch_bounds__(64 * KS) void attn_dv_f32_kernel(const float* __res
   }
 }
 
+// The train step's dV for small problems, the counterpart of
+// attn_fwd_f32_q16_kernel: one workgroup per 16-key block and 16 waves taking
+// its 16-query tiles w, w + KS, ... with v_mfma_f32_16x16x4_f32.  Scores are
+// S = Q . K^T per tile, lane l holding queries 4g + i (g = l / 16) of key
+// l % 16; dV^T += dO^T . P takes queries {4g + s} in k-step s, so each lane
+// feeds its own probability as the B operand and reads dO row 4g + s.  The
+// KS partial dV^T tiles are summed in wave order by all threads, each owning
+// one (d, key) element, which then updates V.  D <= 64, D % 4 == 0, 16-byte
+// aligned operands.
+template <int DQ, int KS>
+__global__ __launch_bounds__(64 * KS) void attn_dv_f32_q16_kernel(const float* __restrict__ q,
+                                                                  const float* __restrict__ k, float* __restrict__ v,
+                                                                  const float* __restrict__ out,
+                                                                  const float* __restrict__ target,
+                                                                  const float* __restrict__ stats, int S, int D,
+                                                                  int causal, float scale, float lr) {
+  constexpr int DP = 16 * DQ;
+  constexpr int QS = DP + 4;              // Q / K row stride
+  constexpr int QO = 16 * QS + 16 * DP;   // floats of one wave's Q + dO tile
+  static_assert(DQ >= 1 && DQ <= 4 && 16 * DP <= QO, "tile");
+  __shared__ __attribute__((aligned(16))) float Ks[16 * QS];
+  __shared__ __attribute__((aligned(16))) float qo[KS][QO];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  float* Qs = &qo[wave][0];
+  float* Gs = &qo[wave][16 * QS];
+  const int j0 = blockIdx.x * 16;  // first key of this block
+  const size_t head = static_cast<size_t>(blockIdx.y) * S * D;
+  q += head;
+  k += head;
+  v += head;
+  out += head;
+  target += head;
+  stats += static_cast<size_t>(blockIdx.y) * S * 2;
+  const float g2 = 2.0f / (static_cast<float>(S) * static_cast<float>(D));
+
+  for (int idx = threadIdx.x; idx < 16 * (DP / 4); idx += 64 * KS) {
+    const int r = idx / (DP / 4);
+    const int cc = (idx - r * (DP / 4)) * 4;
+    *reinterpret_cast<float4*>(&Ks[r * QS + cc]) =
+        (j0 + r < S && cc < D) ? *reinterpret_cast<const float4*>(k + static_cast<size_t>(j0 + r) * D + cc)
+                               : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  __syncthreads();
+
+  floatx4 dv[DQ];
+#pragma unroll
+  for (int t = 0; t < DQ; ++t) {
+    dv[t] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+  const int key = j0 + c;
+  const int nqt = (S + 15) / 16;
+  // Causal: query tile I meets key block J only when I >= J.
+  for (int qt = (causal ? blockIdx.x : 0) + wave; qt < nqt; qt += KS) {
+    const int i0 = qt * 16;
+    // This lane's 4 queries' softmax statistics, loaded first so their
+    // latency overlaps the tile fills and QK^T.
+    float sm[4];
+    float sl[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qi = min(i0 + 4 * g + i, S - 1);
+      sm[i] = stats[static_cast<size_t>(qi) * 2];
+      sl[i] = stats[static_cast<size_t>(qi) * 2 + 1];
+    }
+#pragma unroll
+    for (int t = 0; t < DQ; ++t) {
+      const int idx = t * 64 + lane;
+      const int r = idx / (DP / 4);
+      const int cc = (idx - r * (DP / 4)) * 4;
+      float4 qv = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      float4 gv = qv;
+      if (i0 + r < S && cc < D) {
+        const size_t off = static_cast<size_t>(i0 + r) * D + cc;
+        qv = *reinterpret_cast<const float4*>(q + off);
+        const float4 ov = *reinterpret_cast<const float4*>(out + off);
+        const float4 tv = *reinterpret_cast<const float4*>(target + off);
+        gv = make_float4((ov.x - tv.x) * g2, (ov.y - tv.y) * g2, (ov.z - tv.z) * g2, (ov.w - tv.w) * g2);
+      }
+      *reinterpret_cast<float4*>(&Qs[r * QS + cc]) = qv;
+      *reinterpret_cast<float4*>(&Gs[r * DP + cc]) = gv;
+    }
+    __builtin_amdgcn_wave_barrier();
+    // S = Q . K^T: A = Q rows (query), B = K^T (key); lane group g reduces d
+    // in [g DP/4, (g+1) DP/4).
+    floatx4 st = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    {
+      const float* qrow = &Qs[c * QS + g * (DP / 4)];
+      const float* krow = &Ks[c * QS + g * (DP / 4)];
+#pragma unroll
+      for (int t4 = 0; t4 < DP / 4; t4 += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(qrow + t4);
+        const float4 b4 = *reinterpret_cast<const float4*>(krow + t4);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, st, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qi = i0 + 4 * g + i;
+      float p = 0.0f;
+      if (qi < S && key < S && !(causal && key > qi)) {
+        p = exp2f((st[i] * scale) * kLog2e - sm[i]) / sl[i];
+      }
+      st[i] = p;
+    }
+    // dV^T += dO^T . P: k-step s takes queries {4g + s}.
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int t = 0; t < DQ; ++t) {
+        const float a = Gs[(4 * g + s) * DP + t * 16 + c];
+        dv[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, st[s], dv[t], 0, 0, 0);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // the next query tile overwrites Q / dO
+  }
+
+  // Sum the KS partial dV^T tiles ([d][key], rows d = 16 t + 4 g + i) in wave
+  // order; thread (d, key) then updates V[key][d].
+  float* mine = &qo[wave][0];
+#pragma unroll
+  for (int t = 0; t < DQ; ++t) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      mine[(t * 16 + 4 * g + i) * 16 + c] = dv[t][i];
+    }
+  }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < 16 * DP; idx += 64 * KS) {
+    const int d = idx >> 4;
+    const int kc = idx & 15;
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < KS; ++w) {
+      acc += qo[w][idx];
+    }
+    if (d < D && j0 + kc < S) {
+      float* vp = v + static_cast<size_t>(j0 + kc) * D + d;
+      *vp = *vp - lr * acc;
+    }
+  }
+}
+
 // loss = sum over n elements of (out - target)^2 * norm, one workgroup,
 // fixed reduction order (deterministic).
 __global__ __launch_bounds__(1024) void mse_loss_kernel(const float* __restrict__ out,
@@ -1466,13 +1614,30 @@ hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const 
     return hipErrorInvalidValue;
   }
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
+  const int cz = causal ? 1 : 0;
+  // The 16-key-block kernel under the forward's rule (asked for, or by
+  // default while its grid is at most one workgroup per CU).
+  const bool dflt = splits == 0 && attentionF32DefaultSplits(bh, S, D) == kAttnF32Q16;
+  const bool aligned = reinterpret_cast<uintptr_t>(out) % 16 == 0 && reinterpret_cast<uintptr_t>(target) % 16 == 0;
+  if ((splits == kAttnF32Q16 || dflt) && aligned && attentionF32Q16Fits(D, k, v, q)) {
+    const dim3 grid16((S + 15) / 16, bh);
+#define LC_DV_Q16(DQ_)                                                                                              \
+  hipLaunchKernelGGL((attn_dv_f32_q16_kernel<DQ_, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, target, stats, \
+                     S, D, cz, scale, lr)
+    switch ((D + 15) / 16) {
+      case 1: LC_DV_Q16(1); break;
+      case 2: LC_DV_Q16(2); break;
+      case 3: LC_DV_Q16(3); break;
+      default: LC_DV_Q16(4); break;
+    }
+#undef LC_DV_Q16
+    return hipGetLastError();
+  }
   const int nkb = (S + 31) / 32;
   const dim3 grid(nkb, bh);
   const int dt = (D + 31) / 32;
-  const int cz = causal ? 1 : 0;
   // Query-tile splits: the same rule and LDS limits as the forward's key
-  // splits (K tile + per-wave Q / dO tiles); the forward-only 16-query
-  // variant has no dV counterpart and reads as the heuristic.
+  // splits (K tile + per-wave Q / dO tiles).
   const int ks = attentionF32Splits(bh, S, D, splits == kAttnF32Q16 ? 0 : splits);
 #define LC_DV_F32(DT_, KS_)                                                                                         \
   hipLaunchKernelGGL((attn_dv_f32_kernel<DT_, KS_>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out, target, stats, \

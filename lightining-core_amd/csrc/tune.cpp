@@ -14,8 +14,8 @@
 // shared with the reference keeps its rows.  gfx950 attention rows use their
 // own kinds (HF forward, HT train step), which the reference's reader skips,
 // and carry the arch; the value is the fp32 kernel's split count (1, 2, 4, 8,
-// or 16 on forward rows for the 16-query kernel), and a row whose value is
-// not one of those is dropped.
+// or 16 for the 16-query / 16-key kernels), and a row whose value is not one
+// of those is dropped.
 //
 // The runtime profile autoload restates src/runtime.cpp:101-168.
 #include <algorithm>
@@ -242,7 +242,7 @@ const char* kAttnColumns = "#columns,kind,seq,dim,causal,resident_hint,sync_hint
 const char* kAttnHipColumns = "#columns_hip,kind,seq,dim,causal,resident_hint,sync_hint,compute_loss(HT),arch,splits";
 
 bool validSplit(int mode) { return mode == 1 || mode == 2 || mode == 4 || mode == 8; }
-bool validSplit(char kind, int mode) { return validSplit(mode) || (kind == 'F' && mode == 16); }
+bool validSplit(char, int mode) { return validSplit(mode) || mode == 16; }
 
 std::string joinCsv(const std::vector<std::string>& c) {
   std::string joined;
@@ -273,7 +273,7 @@ bool parseAttn(const std::string& path, std::map<AKey, int>* table, std::vector<
         }
       } else if (c.size() == 9 && c[0] == "HT") {
         const int mode = std::stoi(c[8]);
-        if (validSplit(mode)) {
+        if (validSplit('T', mode)) {
           (*table)[AKey{'T', std::stoull(c[1]), std::stoull(c[2]), std::stoi(c[3]), std::stoi(c[4]),
                         std::stoi(c[5]), std::stoi(c[6]), c[7]}] = mode;
         }

@@ -221,3 +221,53 @@ def test_forced_attention_splits(lc, oracle, tmp_path, s, d, causal):
         err = np.abs(got - ref).max() / np.abs(ref).max()
         note(f"[parity] forced attention splits={ks} S={s} D={d} causal={causal} normwise={err:.3e}")
         assert err <= 1e-4
+
+
+@pytest.mark.parametrize("s,d,causal", [(256, 64, False), (100, 32, True), (1000, 64, False), (33, 20, True)])
+def test_forced_train_dv_splits(lc, oracle, tmp_path, s, d, causal):
+    """Every dV variant of the train step, forced through HT rows (16: the
+    16-key-block kernel), against the oracle's step: updated V, output, loss."""
+    caches = []
+    for ks in (1, 2, 4, 8, 16):
+        cache = tmp_path / f"train_{ks}.csv"
+        rows = [f"HT,{s},{d},{int(causal)},{rh},{sy},{cl},gfx950,{ks}"
+                for rh in (0, 1) for sy in (0, 1) for cl in (0, 1)]
+        cache.write_text("#lc_tune_cache,attention,2\n" + "\n".join(rows) + "\n")
+        caches.append((ks, str(cache)))
+    lr = 3.0
+    out = _child(f"""
+        import json
+        import numpy as np
+        import lightning_core as lc
+        from lightning_core import synth
+        q, k, v, t = (synth.normal(({s}, {d}), stream=700 + i) for i in range(4))
+        for ks, cache in {caches!r}:
+            print("[case] dV splits", ks, flush=True)
+            lc.attention_tune_cache_load(cache)
+            sess = lc.AttentionSession({s}, {d}, causal={causal})
+            o, vn, loss = sess.train_step(q, k, v.copy(), t, {lr})
+            sess.close()
+            print("OUT", ks, json.dumps([np.asarray(vn).ravel().tolist(), np.asarray(o).ravel().tolist(),
+                                         float(loss)]), flush=True)
+    """, tmp_path)
+    q, k, v, t = (synth.normal((s, d), stream=700 + i) for i in range(4))
+    ref_out, ref_v, ref_loss = oracle.attention_train_step(q, k, v, t, lr, causal)
+    outs = [l for l in out.splitlines() if l.startswith("OUT")]
+    assert len(outs) == 5
+    for line in outs:
+        _, ks, payload = line.split(" ", 2)
+        vn, o, loss = json.loads(payload)
+        vn = np.asarray(vn, np.float64)
+        o = np.asarray(o, np.float32)
+        # the V check is relative to the update (V itself is much larger), as
+        # in test_gpu_attention_train.py
+        v0 = np.asarray(v, np.float64).ravel()
+        vr = np.asarray(ref_v, np.float64).ravel()
+        upd = np.abs(vr - v0).max()
+        ev = np.abs(vn - vr).max()
+        eo = np.abs(o - np.asarray(ref_out).ravel()).max() / np.abs(np.asarray(ref_out)).max()
+        note(f"[parity] forced dV splits={ks} S={s} D={d} causal={causal} v err {ev / upd:.2e} of the update, "
+             f"out={eo:.3e}, loss {loss:.6g} vs {float(ref_loss):.6g}")
+        assert ev <= 1e-3 * upd + 4 * np.finfo(np.float32).eps * np.abs(v0).max()
+        assert eo <= 1e-4
+        assert abs(loss - float(ref_loss)) <= 1e-4 * abs(float(ref_loss))

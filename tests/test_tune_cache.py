@@ -124,7 +124,7 @@ def test_attention_cache_seed_and_rows(tmp_path):
         "HF,96,48,0,0,0,gfx950,3",   # not a gfx950 split count: dropped
         "HT,96,48,0,0,0,gfx950,1",   # HT row without compute_loss: ignored
         "HF,128,32,0,0,0,gfx950,16",  # the 16-query forward kernel: kept
-        "HT,128,32,0,0,0,1,gfx950,16",  # no 16-query dV kernel: dropped
+        "HT,128,32,0,0,0,1,gfx950,16",  # the 16-key dV kernel: kept
     ]) + "\n", encoding="utf-8")
     out1 = tmp_path / "attn_out1.csv"
     out2 = tmp_path / "attn_out2.csv"
@@ -134,7 +134,7 @@ def test_attention_cache_seed_and_rows(tmp_path):
         assert lc.attention_tune_cache_size() == 0
         lc.attention_tune_cache_save({str(out1)!r})
         lc.attention_tune_cache_load({str(rows)!r})
-        assert lc.attention_tune_cache_size() == 5, lc.attention_tune_cache_size()
+        assert lc.attention_tune_cache_size() == 6, lc.attention_tune_cache_size()
         lc.attention_tune_cache_save({str(out2)!r})
         lc.attention_reset_tuning()
         assert lc.attention_tune_cache_size() == 0
@@ -145,7 +145,7 @@ def test_attention_cache_seed_and_rows(tmp_path):
     assert l1[2].startswith("#columns_hip,") and len(l1) == 3
     assert sorted(_lines(out2)[3:]) == sorted(["HF,256,64,0,1,0,gfx950,4", "HF,2048,128,1,0,1,gfx950,2",
                                                "HT,256,64,1,0,1,1,gfx950,8", "HF,256,64,0,1,0,gfx942,2",
-                                               "HF,128,32,0,0,0,gfx950,16"])
+                                               "HF,128,32,0,0,0,gfx950,16", "HT,128,32,0,0,0,1,gfx950,16"])
 
 
 def test_attention_cache_keeps_reference_rows(tmp_path):
