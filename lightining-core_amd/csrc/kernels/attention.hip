@@ -212,12 +212,13 @@ struct AttnSrcConvRepeat {
   __device__ float ld(const float* buf, Pos p) const { return buf[p]; }
 };
 
-// Fills rows row0, row0 + rstep, ... (< 32) of 32 x DP tiles (row stride
+// Fills rows row0, row0 + rstep, ... (< ROWS) of ROWS x DP tiles (row stride
 // ldd) with operands W0 (and W1 when NT = 2) of rows first + r of one head;
 // rows >= S and columns >= D are zero.  Lane l covers column l (and l + 64,
-// ...) of a row, or for DP = 32 a column of one of two adjacent rows.  The
-// operands share positions: their loads are issued together.
-template <int DP, int NT, int W0, int W1, typename Src>
+// ...) of a row, or for DP < 64 a column of one of 64 / DP adjacent rows
+// (DP = 48: lanes 48-63 repeat columns 0-15 of the next row, the same value).
+// The operands share positions: their loads are issued together.
+template <int DP, int NT, int W0, int W1, typename Src, int ROWS = 32>
 __device__ inline void fill_rows(const Src& src, const float* buf, float* dst0, int ldd0, float* dst1, int ldd1,
                                  int row0, int rstep, int first, int S, int D, size_t head, int lane) {
   constexpr int RPI = DP >= 64 ? 1 : 64 / DP;
@@ -241,7 +242,7 @@ __device__ inline void fill_rows(const Src& src, const float* buf, float* dst0, 
     dch[ch] = src.delta(static_cast<size_t>(64 * ch));
   }
 #pragma unroll 8
-  for (int r = r0; r < 32; r += rstride) {
+  for (int r = r0; r < ROWS; r += rstride) {
     const bool rok = first + r < S;
 #pragma unroll
     for (int ch = 0; ch < CPR; ++ch) {
@@ -532,13 +533,11 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
 // keys {4g + s}, so each lane feeds its own probability st[s] as the B operand
 // and reads V row 4g + s; output row d = 16 dt + 4g + i, column c.
 // ---------------------------------------------------------------------------
-template <int DQ, int KS>
-__global__ __launch_bounds__(64 * KS) void attn_fwd_f32_q16_kernel(const float* __restrict__ q,
-                                                                   const float* __restrict__ k,
-                                                                   const float* __restrict__ v,
-                                                                   float* __restrict__ out, float* __restrict__ stats,
-                                                                   int S, int D, int causal, float scale,
-                                                                   float post_scale, float post_bias, int post_relu) {
+template <int DQ, int KS, typename Src>
+__global__ __launch_bounds__(64 * KS) void attn_fwd_f32_q16_kernel(Src src, float* __restrict__ out,
+                                                                   float* __restrict__ stats, int S, int D,
+                                                                   int causal, float scale, float post_scale,
+                                                                   float post_bias, int post_relu) {
   constexpr int DP = 16 * DQ;
   constexpr int QS = DP + 4;             // Q / K row stride (16-byte aligned rows)
   constexpr int KVF = 16 * QS + 16 * DP; // floats of one wave's K + V tile
@@ -546,6 +545,7 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_q16_kernel(const float* 
   static_assert(DQ >= 1 && DQ <= 4 && 32 + 16 * PS <= KVF, "tile");
   __shared__ __attribute__((aligned(16))) float Qs[16 * QS];
   __shared__ __attribute__((aligned(16))) float kv[KS][KVF];
+  __shared__ float srcbuf[Src::kLds > 0 ? Src::kLds : 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int g = lane >> 4;
@@ -559,31 +559,41 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_q16_kernel(const float* 
   const int kend = causal ? min(S, q0 + 16) : S;
   const int jfirst = wave * 16;
   constexpr int jstep = 16 * KS;
+  src.prologue(srcbuf, 64 * KS);
 
-  // One tile of K and V is 16 rows x DP/4 float4: DQ chunks per lane each.
-  float4 kr[DQ], vr[DQ];
+  // Global sources (Src::kVec): one tile of K and V is 16 rows x DP/4
+  // float4, DQ chunks per lane each, prefetched one tile ahead in registers.
+  // Other sources fill the tiles through the source's positions.
+  constexpr bool VEC = Src::kVec;
+  float4 kr[VEC ? DQ : 1], vr[VEC ? DQ : 1];
   auto fetch = [&](int j0) {
+    if constexpr (VEC) {
 #pragma unroll
-    for (int t = 0; t < DQ; ++t) {
-      const int idx = t * 64 + lane;  // row idx / (DP/4), column 4 (idx % (DP/4))
-      const int r = idx / (DP / 4);
-      const int cc = (idx - r * (DP / 4)) * 4;
-      const bool ok = j0 + r < S && cc < D;
-      const size_t off = head + static_cast<size_t>(j0 + r) * D + cc;
-      kr[t] = ok ? *reinterpret_cast<const float4*>(k + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-      vr[t] = ok ? *reinterpret_cast<const float4*>(v + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      for (int t = 0; t < DQ; ++t) {
+        const int idx = t * 64 + lane;  // row idx / (DP/4), column 4 (idx % (DP/4))
+        const int r = idx / (DP / 4);
+        const int cc = (idx - r * (DP / 4)) * 4;
+        const bool ok = j0 + r < S && cc < D;
+        const size_t off = head + static_cast<size_t>(j0 + r) * D + cc;
+        kr[t] = ok ? *reinterpret_cast<const float4*>(src.k + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        vr[t] = ok ? *reinterpret_cast<const float4*>(src.v + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      }
     }
   };
-  if (jfirst < kend) {
-    fetch(jfirst);  // out before the Q loads, so the latencies overlap
-  }
-  for (int idx = threadIdx.x; idx < 16 * (DP / 4); idx += 64 * KS) {
-    const int r = idx / (DP / 4);
-    const int cc = (idx - r * (DP / 4)) * 4;
-    const bool ok = q0 + r < S && cc < D;
-    *reinterpret_cast<float4*>(&Qs[r * QS + cc]) =
-        ok ? *reinterpret_cast<const float4*>(q + head + static_cast<size_t>(q0 + r) * D + cc)
-           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  if constexpr (VEC) {
+    if (jfirst < kend) {
+      fetch(jfirst);  // out before the Q loads, so the latencies overlap
+    }
+    for (int idx = threadIdx.x; idx < 16 * (DP / 4); idx += 64 * KS) {
+      const int r = idx / (DP / 4);
+      const int cc = (idx - r * (DP / 4)) * 4;
+      const bool ok = q0 + r < S && cc < D;
+      *reinterpret_cast<float4*>(&Qs[r * QS + cc]) =
+          ok ? *reinterpret_cast<const float4*>(src.q + head + static_cast<size_t>(q0 + r) * D + cc)
+             : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+  } else {
+    fill_rows<DP, 1, 0, 0, Src, 16>(src, srcbuf, Qs, QS, nullptr, 0, wave, KS, q0, S, D, head, lane);
   }
   __syncthreads();
 
@@ -595,16 +605,20 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_q16_kernel(const float* 
   float m_run = kMaskValue;
   float l_run = 0.0f;
   for (int j0 = jfirst; j0 < kend; j0 += jstep) {
+    if constexpr (VEC) {
 #pragma unroll
-    for (int t = 0; t < DQ; ++t) {
-      const int idx = t * 64 + lane;
-      const int r = idx / (DP / 4);
-      const int cc = (idx - r * (DP / 4)) * 4;
-      *reinterpret_cast<float4*>(&Ks[r * QS + cc]) = kr[t];
-      *reinterpret_cast<float4*>(&Vs[r * DP + cc]) = vr[t];
-    }
-    if (j0 + jstep < kend) {
-      fetch(j0 + jstep);
+      for (int t = 0; t < DQ; ++t) {
+        const int idx = t * 64 + lane;
+        const int r = idx / (DP / 4);
+        const int cc = (idx - r * (DP / 4)) * 4;
+        *reinterpret_cast<float4*>(&Ks[r * QS + cc]) = kr[t];
+        *reinterpret_cast<float4*>(&Vs[r * DP + cc]) = vr[t];
+      }
+      if (j0 + jstep < kend) {
+        fetch(j0 + jstep);
+      }
+    } else {
+      fill_rows<DP, 2, 1, 2, Src, 16>(src, srcbuf, Ks, QS, Vs, DP, 0, 1, j0, S, D, head, lane);
     }
     __builtin_amdgcn_wave_barrier();  // only this wave reads its K / V tile
 
@@ -1491,24 +1505,17 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
   const bool dflt = splits == 0 && attentionF32DefaultSplits(bh, S, D) == kAttnF32Q16;
   if ((splits == kAttnF32Q16 || dflt) && attentionF32Q16Fits(D, k, v, q)) {
     const dim3 grid16((S + 15) / 16, bh);
+    const AttnSrcGlobal gsrc{q, k, v};
+#define LC_ATTN_Q16(DQ_)                                                                                            \
+  hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<DQ_, 16, AttnSrcGlobal>), grid16, dim3(1024), 0, stream, gsrc, out,   \
+                     stats, S, D, cz, scale, post_scale, post_bias, post_relu)
     switch ((D + 15) / 16) {
-      case 1:
-        hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<1, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, stats, S, D,
-                           cz, scale, post_scale, post_bias, post_relu);
-        break;
-      case 2:
-        hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<2, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, stats, S, D,
-                           cz, scale, post_scale, post_bias, post_relu);
-        break;
-      case 3:
-        hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<3, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, stats, S, D,
-                           cz, scale, post_scale, post_bias, post_relu);
-        break;
-      default:
-        hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<4, 16>), grid16, dim3(1024), 0, stream, q, k, v, out, stats, S, D,
-                           cz, scale, post_scale, post_bias, post_relu);
-        break;
+      case 1: LC_ATTN_Q16(1); break;
+      case 2: LC_ATTN_Q16(2); break;
+      case 3: LC_ATTN_Q16(3); break;
+      default: LC_ATTN_Q16(4); break;
     }
+#undef LC_ATTN_Q16
     return hipGetLastError();
   }
   const int nqb = (S + 31) / 32;
@@ -1575,6 +1582,22 @@ hipError_t convAttentionF32(const float* x, const float* w, const float* bias, i
                         static_cast<int>(xs < big ? xs : big), static_cast<int>(ws < big ? ws : big),
                         static_cast<size_t>(S) * D};
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
+  // D <= 64: the 16-query kernel (16 waves of 16-key tiles, 8 at D > 48 so
+  // that the per-wave tiles fit next to the conv buffer).
+  if (D <= 64) {
+    const dim3 grid16((S + 15) / 16, 1);
+#define LC_CA_Q16(DQ_, KS_)                                                                                         \
+  hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<DQ_, KS_, AttnSrcConvRepeat>), grid16, dim3(64 * (KS_)), 0, stream,   \
+                     src, out, nullptr, S, D, 0, scale, 1.0f, 0.0f, 0)
+    switch ((D + 15) / 16) {
+      case 1: LC_CA_Q16(1, 16); break;
+      case 2: LC_CA_Q16(2, 16); break;
+      case 3: LC_CA_Q16(3, 16); break;
+      default: LC_CA_Q16(4, 8); break;
+    }
+#undef LC_CA_Q16
+    return hipGetLastError();
+  }
   const int nqb = (S + 31) / 32;
   const dim3 grid(nqb, 1);
   const int dt = (D + 31) / 32;
