@@ -288,6 +288,13 @@ Status vitValidate(const lcVitBlockConfig& c) {
   return Status::kSuccess;
 }
 
+// The fused QKV + attention kernel is the default where it fits;
+// CJ_HIP_VIT_FUSED=0 selects the separate QKV GEMM and attention kernels.
+bool vitFusedEnabled() {
+  const char* env = getenv("CJ_HIP_VIT_FUSED");
+  return env == nullptr || std::string(env) != "0";
+}
+
 Status vitForwardDevice(HipContext* ctx, lcVitBlockSession* s) {
   const auto& c = s->cfg;
   const kern::Half ht = halfOf(c.compute_dtype);
@@ -304,6 +311,20 @@ Status vitForwardDevice(HipContext* ctx, lcVitBlockSession* s) {
     return failHip(e, "vit patch-embed launch");
   }
   traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, s->M * c.embed * 3 * c.embed);
+  if (vitFusedEnabled() && kern::vitQkvAttentionFits(T, E, H)) {
+    // QKV projection and attention in one launch per (image, head): Q, K and
+    // V^T stay in LDS.
+    traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, s->T * s->T * s->Dh);
+    e = kern::vitQkvAttention(s->tokens16.as<uint16_t>(), s->wqkv_t16.as<uint16_t>(), s->attn16.as<uint16_t>(), B, T,
+                              E, H, ht, ctx->stream);
+    if (e != hipSuccess) {
+      return failHip(e, "vit qkv + attention launch");
+    }
+    traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, s->M * c.embed * c.embed);
+    e = kern::outProjectGemm(s->attn16.as<uint16_t>(), s->wo_t16.as<uint16_t>(), s->out.as<float>(), M, E, ht,
+                             ctx->stream);
+    return e == hipSuccess ? Status::kSuccess : failHip(e, "vit out-projection launch");
+  }
   e = kern::qkvProjectGemm(s->tokens16.as<uint16_t>(), s->wqkv_t16.as<uint16_t>(), s->q16.as<uint16_t>(),
                            s->k16.as<uint16_t>(), s->vt16.as<uint16_t>(), B, T, E, H, static_cast<int>(s->S_pad), ht,
                            ctx->stream);

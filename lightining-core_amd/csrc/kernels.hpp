@@ -193,4 +193,11 @@ hipError_t attentionHalf(const uint16_t* q, const uint16_t* k, const uint16_t* v
                          uint16_t* out_heads_concat, int heads, int bh, int S, int S_pad, int D, bool causal, Half t,
                          hipStream_t stream);
 
+// ViT: QKV projection of each (image, head) fused with its attention
+// (vit_qkv_attn_kernel); tokens [B*T][E], Wqkv_t [3E][E], output
+// heads-concatenated [B*T][E].  Needs E / H == 64, T <= 256, E % 64 == 0.
+bool vitQkvAttentionFits(int T_, int E, int H);
+hipError_t vitQkvAttention(const uint16_t* tokens, const uint16_t* Wqkv_t, uint16_t* out_heads_concat, int B,
+                           int T_, int E, int H, Half t, hipStream_t stream);
+
 }  // namespace lchip::kern

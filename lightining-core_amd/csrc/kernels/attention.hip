@@ -17,6 +17,8 @@
 // evaluated as exp2 with log2(e) folded into the scale (online form).
 #include <math.h>
 
+#include <type_traits>
+
 #include "../kernels.hpp"
 #include "kcommon.hpp"
 
@@ -1135,6 +1137,245 @@ __device__ __forceinline__ u32x4 scale_halves(u32x4 v, float c) {
   return r;
 }
 
+// Per-wave state and steps of the 16-bit attention: queries q0 .. q0 + 31
+// against 64-key K / V^T tiles in LDS, in the layouts above.  Shared by
+// attn_fwd_half_kernel (tiles streamed through two LDS buffers) and
+// vit_qkv_attn_kernel (every tile resident), so both compute the same values.
+template <typename T, int D>
+struct HalfAttnWave {
+  static constexpr int KT = 64;
+  static constexpr int KCH = D / 8;  // 16-byte chunks per K row
+  static constexpr int DT = D / 32;
+  static constexpr int QS = D / 16;
+  static_assert(D == 64 || D == 128, "head dim");
+  u32x4 qf[QS];
+  floatx16 o[DT];
+  // Scores are kept relative to a per-query reference m_run (exp2 units): the
+  // QK^T MFMAs start from -m_run instead of zero, so x = s*c - m_run comes
+  // out of the accumulator and p = exp2(x) needs no extra arithmetic.  The
+  // reference moves to the tile max on a query's first tile with a valid key,
+  // and later only when the max exceeds it by more than 8 (then O, l and the
+  // tile's scores are shifted); exponents stay <= 8.
+  float m_run;
+  float l_run;
+  bool started;
+  int lrow;
+  int half;
+  int prow;
+  int kswz;
+  int vswz;
+  int q0;
+  int qi;
+  int S;
+  int causal;
+
+  // qrow: this lane's Q row (query q0 + lane % 32), D contiguous values.  Q
+  // fragments are pre-multiplied by c = scale * log2(e) (rounded back to the
+  // 16-bit type once per wave), so the QK^T MFMAs produce scores in exp2 units.
+  __device__ __forceinline__ void init(const uint16_t* qrow, int q0_, int S_, int causal_, float scale, int lane) {
+    lrow = lane & 31;
+    half = lane >> 5;
+    q0 = q0_;
+    qi = q0 + lrow;
+    S = S_;
+    causal = causal_;
+    const float c = scale * kLog2e;
+#pragma unroll
+    for (int s = 0; s < QS; ++s) {
+      qf[s] = scale_halves<T>(*reinterpret_cast<const u32x4*>(qrow + s * 16 + 8 * half), c);
+    }
+    // Fragment addresses (elements).  K: MFMA row lrow of 32-key block kt
+    // reads key kt*32 + pi(lrow); its swizzle does not depend on kt.
+    prow = (lrow & ~12) | ((lrow & 4) << 1) | ((lrow & 8) >> 1);
+    kswz = KCH == 16 ? (prow & 15) : ((prow >> 1) & 7);
+    vswz = (lrow >> 1) & 7;
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      o[t] = zero16();
+    }
+    m_run = 0.0f;
+    l_run = 0.0f;
+    started = false;
+  }
+
+  // Raw scores of the K tile at ks (two 32-key blocks).
+  __device__ __forceinline__ void qk(const uint16_t* ks, floatx16 (&sc)[2]) const {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      sc[kt] = zero16();
+#pragma unroll
+      for (int s = 0; s < QS; ++s) {
+        const u32x4 a =
+            *reinterpret_cast<const u32x4*>(ks + (kt * 32 + prow) * D + (((2 * s + half) ^ kswz) << 3));
+        sc[kt] = mfma32x32x16<T>(a, qf[s], sc[kt]);
+      }
+    }
+  }
+
+  // Tile j's probabilities from its raw scores s_cur (p = exp2(s*c - m*c), m
+  // the running max of raw scores), with the next tile's QK^T MFMAs (K tile
+  // at ksn) in the same basic block so the scheduler interleaves them with the
+  // VALU work, then tile j's O^T += V^T . P^T (V^T tile at vs).
+  __device__ __forceinline__ void step(int j, const uint16_t* ksn, const uint16_t* vs, floatx16 (&s_cur)[2],
+                                       floatx16 (&s_nxt)[2]) {
+      const int j0 = j * KT;
+      if ((j0 + KT > S) || (causal && j0 + KT - 1 > q0)) {
+        // key = j0 + 8*half + off with off a compile-time constant per register;
+        // masked when key >= S or (causal) key > qi, i.e. off > lim.
+        const int lim = (causal ? min(qi, S - 1) : S - 1) - j0 - 8 * half;
+  #pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            if (kt * 32 + 16 * (i >> 3) + (i & 7) > lim) {
+              s_cur[kt][i] = kMaskValue;
+            }
+          }
+        }
+      }
+      float mt = kMaskValue;
+  #pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+  #pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          mt = fmaxf(mt, s_cur[kt][i]);
+        }
+      }
+      mt = max_xor32(mt);
+      // Lanes l and l ^ 32 hold the same query and see the same mt, so their
+      // references stay equal.  O and l always share the reference, so O/l is
+      // unchanged by a shift.
+      const bool valid = mt > 0.5f * kMaskValue;
+      const bool shift = valid && (!started || mt > 8.0f);
+      started = started || valid;
+      if (__any(shift)) {
+        const float sh = shift ? mt : 0.0f;
+        const float alpha = fast_exp2(-sh);
+        m_run += sh;
+        l_run *= alpha;
+  #pragma unroll
+        for (int t = 0; t < DT; ++t) {
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            o[t][i] *= alpha;
+          }
+        }
+  #pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+  #pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            s_cur[kt][i] -= sh;
+          }
+        }
+      }
+      // Phase 1: the 32 exponentials of this lane, packed to 16-bit pairs as
+      // they come, with the next tile's 2*QS QK^T MFMAs issued between them
+      // (EPM exponentials per MFMA, K fragments read two MFMAs ahead).  The
+      // sched_barrier after each group keeps this order: an MFMA runs for 32
+      // clocks while the wave issues the group's VALU work behind it.
+      constexpr int NQK = 2 * QS;
+      constexpr int EPM = 32 / NQK;
+      floatx16 negm;
+  #pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        negm[i] = -m_run;
+      }
+      float ls = 0.0f;
+      u32x4 pb[4];
+      auto kfrag = [&](int g) {
+        const int kt = g / QS;
+        const int s = g - kt * QS;
+        return *reinterpret_cast<const u32x4*>(ksn + (kt * 32 + prow) * D + (((2 * s + half) ^ kswz) << 3));
+      };
+      // Fragments rotate through a 3-entry ring indexed by the unrolled g
+      // (no register copies).
+      u32x4 kf[3];
+      kf[0] = kfrag(0);
+      kf[1] = kfrag(1);
+  #pragma unroll
+      for (int g = 0; g < NQK; ++g) {
+        if (g + 2 < NQK) {
+          kf[(g + 2) % 3] = kfrag(g + 2);
+        }
+        {
+          const int kt = g / QS;
+          const int s = g - kt * QS;
+          s_nxt[kt] = mfma32x32x16<T>(kf[g % 3], qf[s], s == 0 ? negm : s_nxt[kt]);
+        }
+  #pragma unroll
+        for (int e = 0; e < EPM; e += 2) {
+          const int idx = g * EPM + e;  // score element idx and idx + 1
+          const float p0 = fast_exp2(s_cur[idx >> 4][idx & 15]);
+          const float p1 = fast_exp2(s_cur[idx >> 4][(idx & 15) + 1]);
+          const uint32_t pair = pack2<T>(p0, p1);
+          // l sums the rounded probabilities the P.V MFMAs consume.
+          ls = add_pair<T>(pair, ls);
+          pb[idx >> 3][(idx & 7) >> 1] = pair;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      l_run += ls;
+      // Phase 2: O^T += V^T . P^T, V^T fragments read two MFMAs ahead.
+      auto vfrag = [&](int g) {
+        const int ks2 = g / DT;
+        const int t = g - ks2 * DT;
+        return *reinterpret_cast<const u32x4*>(vs + (t * 32 + lrow) * KT + (((2 * ks2 + half) ^ vswz) << 3));
+      };
+      constexpr int NPV = 4 * DT;
+      u32x4 vf[3];
+      vf[0] = vfrag(0);
+      vf[1] = vfrag(1);
+  #pragma unroll
+      for (int g = 0; g < NPV; ++g) {
+        if (g + 2 < NPV) {
+          vf[(g + 2) % 3] = vfrag(g + 2);
+        }
+        const int ks2 = g / DT;
+        const int t = g - ks2 * DT;
+        o[t] = mfma32x32x16<T>(vf[g % 3], pb[ks2], o[t]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+  }
+
+  // Normalises and stores this wave's rows: fp32 [bh][S][D] to O, or (O null)
+  // 16-bit heads-concatenated [b][S][heads * D] to Ocat.
+  __device__ __forceinline__ void store(float* __restrict__ O, uint16_t* __restrict__ Ocat, int bh, int heads) const {
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float inv = 1.0f / l_tot;
+    if (qi >= S) {
+      return;
+    }
+    if (Ocat == nullptr) {
+      float* orow = O + (static_cast<size_t>(bh) * S + qi) * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = t * 32 + 8 * g + 4 * half;
+          const float4 val = make_float4(o[t][4 * g] * inv, o[t][4 * g + 1] * inv, o[t][4 * g + 2] * inv,
+                                         o[t][4 * g + 3] * inv);
+          *reinterpret_cast<float4*>(orow + d) = val;
+        }
+      }
+    } else {
+      const int b = bh / heads;
+      const int h = bh - b * heads;
+      uint16_t* orow = Ocat + (static_cast<size_t>(b) * S + qi) * (heads * D) + h * D;
+#pragma unroll
+      for (int t = 0; t < DT; ++t) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d = t * 32 + 8 * g + 4 * half;
+          u32x2 w;
+          w[0] = pack2<T>(o[t][4 * g] * inv, o[t][4 * g + 1] * inv);
+          w[1] = pack2<T>(o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
+          *reinterpret_cast<u32x2*>(orow + d) = w;
+        }
+      }
+    }
+  }
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* __restrict__ Q,
                                                                const uint16_t* __restrict__ K,
@@ -1146,9 +1387,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   constexpr int K_RPI = 64 / KCH;          // K rows per 1 KB load instruction
   constexpr int TILE = KT * D;             // elements of a K (or V^T) tile
   constexpr int LPW = TILE * 2 / 1024 / 4; // load instructions per wave per operand
-  constexpr int DT = D / 32;
-  constexpr int QS = D / 16;
-  static_assert(D == 64 || D == 128, "head dim");
   // One LDS array: K buffers at 0 and TILE, V^T buffers at 2*TILE and
   // 3*TILE (copies address it by byte offset from its base).
   __shared__ __attribute__((aligned(16))) uint16_t smem[4 * TILE];
@@ -1162,8 +1400,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   const int q0 = qb * 128 + wave * 32;
   const size_t hoff = static_cast<size_t>(bh) * S_pad * D;
   const uint16_t* Qh = Q + hoff;
-  const int lrow = lane & 31;
-  const int half = lane >> 5;
 
   // Load mapping: wave w issues instructions w + 4j (j < LPW) of each operand.
   // K instruction i fills rows K_RPI*i + lane / KCH, physical chunk lane % KCH;
@@ -1201,183 +1437,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
     }
   };
 
-  // Q fragments, pre-multiplied by c = scale * log2(e) (rounded back to the
-  // 16-bit type once per wave), so the QK^T MFMAs produce scores in exp2 units.
-  const float c = scale * kLog2e;
-  u32x4 qf[QS];
-#pragma unroll
-  for (int s = 0; s < QS; ++s) {
-    qf[s] = scale_halves<T>(
-        *reinterpret_cast<const u32x4*>(Qh + static_cast<size_t>(q0 + lrow) * D + s * 16 + 8 * half), c);
-  }
-
-  // Fragment addresses (elements).  K: MFMA row lrow of 32-key block kt reads
-  // key kt*32 + pi(lrow); its swizzle does not depend on kt.
-  const int prow = (lrow & ~12) | ((lrow & 4) << 1) | ((lrow & 8) >> 1);
-  const int kswz = KCH == 16 ? (prow & 15) : ((prow >> 1) & 7);
-  const int vswz = (lrow >> 1) & 7;
-  auto qk = [&](const uint16_t* ks, floatx16 (&sc)[2]) {
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      sc[kt] = zero16();
-#pragma unroll
-      for (int s = 0; s < QS; ++s) {
-        const u32x4 a =
-            *reinterpret_cast<const u32x4*>(ks + (kt * 32 + prow) * D + (((2 * s + half) ^ kswz) << 3));
-        sc[kt] = mfma32x32x16<T>(a, qf[s], sc[kt]);
-      }
-    }
-  };
-
-  floatx16 o[DT];
-#pragma unroll
-  for (int t = 0; t < DT; ++t) {
-    o[t] = zero16();
-  }
-  // Scores are kept relative to a per-query reference m_run (exp2 units): the
-  // QK^T MFMAs start from -m_run instead of zero, so x = s*c - m_run comes
-  // out of the accumulator and p = exp2(x) needs no extra arithmetic.  The
-  // reference moves to the tile max on a query's first tile with a valid key,
-  // and later only when the max exceeds it by more than 8 (then O, l and the
-  // tile's scores are shifted); exponents stay <= 8.
-  float m_run = 0.0f;
-  float l_run = 0.0f;
-  bool started = false;
-  const int qi = q0 + lrow;
+  HalfAttnWave<T, D> w;
+  w.init(Qh + static_cast<size_t>(q0 + (lane & 31)) * D, q0, S, causal, scale, lane);
   const int kend = causal ? min(S, qb * 128 + 128) : S;
   const int nt = (kend + KT - 1) / KT;
   // Causal: tile j is skipped by a wave whose queries all precede its keys
   // (monotone in j: a skipped tile is followed only by skipped tiles).
   auto active = [&](int j) { return !(causal && j * KT > q0 + 31); };
 
-  // Tile j's probabilities from its raw scores sc (p = exp2(s*c - m*c), m the
-  // running max of raw scores), optionally with tile j+1's QK^T MFMAs in the
-  // same basic block (so the scheduler interleaves them with the VALU work),
-  // then tile j's O^T += V^T . P^T.
   floatx16 s_a[2];
   floatx16 s_b[2];
-  auto step = [&](int j, floatx16 (&s_cur)[2], floatx16 (&s_nxt)[2]) {
-    const int j0 = j * KT;
-    if ((j0 + KT > S) || (causal && j0 + KT - 1 > q0)) {
-      // key = j0 + 8*half + off with off a compile-time constant per register;
-      // masked when key >= S or (causal) key > qi, i.e. off > lim.
-      const int lim = (causal ? min(qi, S - 1) : S - 1) - j0 - 8 * half;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          if (kt * 32 + 16 * (i >> 3) + (i & 7) > lim) {
-            s_cur[kt][i] = kMaskValue;
-          }
-        }
-      }
-    }
-    float mt = kMaskValue;
-#pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        mt = fmaxf(mt, s_cur[kt][i]);
-      }
-    }
-    mt = max_xor32(mt);
-    // Lanes l and l ^ 32 hold the same query and see the same mt, so their
-    // references stay equal.  O and l always share the reference, so O/l is
-    // unchanged by a shift.
-    const bool valid = mt > 0.5f * kMaskValue;
-    const bool shift = valid && (!started || mt > 8.0f);
-    started = started || valid;
-    if (__any(shift)) {
-      const float sh = shift ? mt : 0.0f;
-      const float alpha = fast_exp2(-sh);
-      m_run += sh;
-      l_run *= alpha;
-#pragma unroll
-      for (int t = 0; t < DT; ++t) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          o[t][i] *= alpha;
-        }
-      }
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          s_cur[kt][i] -= sh;
-        }
-      }
-    }
-    // Phase 1: the 32 exponentials of this lane, packed to 16-bit pairs as
-    // they come, with the next tile's 2*QS QK^T MFMAs issued between them
-    // (EPM exponentials per MFMA, K fragments read two MFMAs ahead).  The
-    // sched_barrier after each group keeps this order: an MFMA runs for 32
-    // clocks while the wave issues the group's VALU work behind it.
-    constexpr int NQK = 2 * QS;
-    constexpr int EPM = 32 / NQK;
-    floatx16 negm;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      negm[i] = -m_run;
-    }
-    float ls = 0.0f;
-    u32x4 pb[4];
-    const uint16_t* ksn = smem + ((j + 1) & 1) * TILE;
-    auto kfrag = [&](int g) {
-      const int kt = g / QS;
-      const int s = g - kt * QS;
-      return *reinterpret_cast<const u32x4*>(ksn + (kt * 32 + prow) * D + (((2 * s + half) ^ kswz) << 3));
-    };
-    // Fragments rotate through a 3-entry ring indexed by the unrolled g
-    // (no register copies).
-    u32x4 kf[3];
-    kf[0] = kfrag(0);
-    kf[1] = kfrag(1);
-#pragma unroll
-    for (int g = 0; g < NQK; ++g) {
-      if (g + 2 < NQK) {
-        kf[(g + 2) % 3] = kfrag(g + 2);
-      }
-      {
-        const int kt = g / QS;
-        const int s = g - kt * QS;
-        s_nxt[kt] = mfma32x32x16<T>(kf[g % 3], qf[s], s == 0 ? negm : s_nxt[kt]);
-      }
-#pragma unroll
-      for (int e = 0; e < EPM; e += 2) {
-        const int idx = g * EPM + e;  // score element idx and idx + 1
-        const float p0 = fast_exp2(s_cur[idx >> 4][idx & 15]);
-        const float p1 = fast_exp2(s_cur[idx >> 4][(idx & 15) + 1]);
-        const uint32_t pair = pack2<T>(p0, p1);
-        // l sums the rounded probabilities the P.V MFMAs consume.
-        ls = add_pair<T>(pair, ls);
-        pb[idx >> 3][(idx & 7) >> 1] = pair;
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    l_run += ls;
-    // Phase 2: O^T += V^T . P^T, V^T fragments read two MFMAs ahead.
-    const uint16_t* vs = smem + (2 + (j & 1)) * TILE;
-    auto vfrag = [&](int g) {
-      const int ks2 = g / DT;
-      const int t = g - ks2 * DT;
-      return *reinterpret_cast<const u32x4*>(vs + (t * 32 + lrow) * KT + (((2 * ks2 + half) ^ vswz) << 3));
-    };
-    constexpr int NPV = 4 * DT;
-    u32x4 vf[3];
-    vf[0] = vfrag(0);
-    vf[1] = vfrag(1);
-#pragma unroll
-    for (int g = 0; g < NPV; ++g) {
-      if (g + 2 < NPV) {
-        vf[(g + 2) % 3] = vfrag(g + 2);
-      }
-      const int ks2 = g / DT;
-      const int t = g - ks2 * DT;
-      o[t] = mfma32x32x16<T>(vf[g % 3], pb[ks2], o[t]);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
-
   issue_k(0, 0);
   issue_v(0, 0);
   if (nt > 1) {
@@ -1385,7 +1454,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
   }
   wait_vmcnt<0>();
   stage_barrier();
-  qk(smem, s_a);     // tile 0 is active for every wave
+  w.qk(smem, s_a);   // tile 0 is active for every wave
   stage_barrier();   // K buffer 0 is refilled next
   // One tile: its loads of K(j+2) and V^T(j+1) go out first, then the
   // pipelined step (the next tile's scores are computed unconditionally, one
@@ -1401,7 +1470,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
       issue_v((j + 1) & 1, j + 1);
     }
     if (active(j)) {
-      step(j, s_cur, s_nxt);
+      w.step(j, smem + ((j + 1) & 1) * TILE, smem + (2 + (j & 1)) * TILE, s_cur, s_nxt);
     }
     wait_vmcnt<0>();  // this wave's loads of K(j+2) and V^T(j+1) have landed
     stage_barrier();  // everyone's have; everyone is done with K(j+1) and V^T(j)
@@ -1412,38 +1481,368 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_half_kernel(const uint16_t* _
       tile(j + 1, s_b, s_a);
     }
   }
+  w.store(O, Ocat, bh, heads);
+}
 
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = 1.0f / l_tot;
-  if (qi < S) {
-    if (Ocat == nullptr) {
-      float* orow = O + (static_cast<size_t>(bh) * S + qi) * D;
+// ---------------------------------------------------------------------------
+// ViT block: the QKV projection of one (image, head) fused with its
+// attention, so Q, K and V^T never leave LDS.  T <= 224 tokens (nrb =
+// ceil(T/32) <= 7 blocks of 32), head dim 64.  Each (image b, head h) takes
+// nparts = min(2, nrb) workgroups of 8 waves; part p owns a contiguous range
+// of query blocks [qlo, qhi) (at most 4), and every part projects K and V for
+// all tokens (the attention of its queries needs every key), Q only for its
+// own queries.
+//  1. Projection: token rows of image b times the head's 192 rows of W_qkv^T
+//     (Q rows h*64.., K rows E + h*64.., V rows 2E + h*64..), in 64-deep
+//     stages through a ring of three LDS buffers: 224 token rows (rows past T
+//     re-read token T-1, so every value stays finite) and the 192 weight
+//     rows, 128-byte rows with chunk ^ ((row >> 1) & 7), one direct
+//     global -> LDS copy per 8 rows (52 per stage, 6 or 7 per wave).  The
+//     copies of stage s+2 go out during stage s, two after each k-step.
+//     32x32 output blocks ("units") per wave: wave w < nrb takes K and V of
+//     token block w (four units) and, when w is one of this part's query
+//     blocks, Q's first 32 columns; Q's other 32 columns of this part's first
+//     min(3, #query blocks) blocks go to wave 7 and those of the rest stay
+//     with their wave (at T = 196 that is 9 units on every SIMD).  Q and K
+//     units compute W . tokens^T (rows d, columns tokens) and V units
+//     tokens . W^T, so every lane ends up with 4 consecutive elements of one
+//     LDS row below.  v_mfma_f32_32x32x16 in the k order of the QKV GEMM, the
+//     fragments of k-step kk+1 read while kk's MFMAs run.
+//  2. The accumulators go to LDS as 16-bit Q [128][64] (this part's queries),
+//     K tiles [64][64] and V^T tiles [64][64] (keys past the last token block
+//     zero) in attn_fwd_half_kernel's layouts, 8-byte stores.
+//  3. Wave a < #query blocks runs attention for query block qlo + a over
+//     every key tile (HalfAttnWave: attn_fwd_half_kernel's arithmetic) and
+//     stores its rows of the heads-concatenated output.
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(512) void vit_qkv_attn_kernel(const uint16_t* __restrict__ tokens,
+                                                          const uint16_t* __restrict__ Wqkv_t,
+                                                          uint16_t* __restrict__ Ocat, int T_, int E, int H,
+                                                          int nparts, float scale) {
+  constexpr int D = 64;
+  constexpr int KT = 64;
+  constexpr int TILE = KT * D;            // elements of a K (or V^T) tile
+  constexpr int AR = 224;                 // token rows per stage (padded)
+  constexpr int WR = 3 * D;               // weight rows: Q, K, V of one head
+  constexpr int NB = 3;                   // ring buffers
+  constexpr int STAGE = (AR + WR) * 64;   // elements per projection stage
+  constexpr int NCP = (AR + WR) / 8;      // 1 KB copies per stage (52)
+  constexpr int CPW = (NCP + 7) / 8;      // per wave, at most (7)
+  constexpr int ACP = AR / 8;             // ... of token rows (28)
+  constexpr int QR = 128;                 // Q rows held (4 query blocks)
+  constexpr int SP = 256;                 // keys held by the K / V^T tiles
+  // Phase 2 layout (elements): Q [QR][D] at 0, then the K tiles, then the
+  // V^T tiles.
+  constexpr int KOFF = QR * D;
+  constexpr int VOFF = KOFF + (SP / KT) * TILE;
+  static_assert(VOFF + (SP / KT) * TILE <= NB * STAGE, "phase 2 fits in the projection ring");
+  static_assert(NB * STAGE * 2 <= 160 * 1024, "LDS");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[NB * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wave_s = __builtin_amdgcn_readfirstlane(wave);
+  const int bh = blockIdx.x / nparts;
+  const int part = blockIdx.x - bh * nparts;
+  const int b = bh / H;
+  const int h = bh - b * H;
+  const uint16_t* tok = tokens + static_cast<size_t>(b) * T_ * E;
+  const int nrb = (T_ + 31) >> 5;
+  const int per = (nrb + nparts - 1) / nparts;
+  const int qlo = part * per;
+  const int nq = min(nrb, qlo + per) - qlo;  // 1..4
+  const int nmove = min(3, nq);              // Q column-block-1 units done by wave 7
+
+  // Copy j of this wave is instruction i = wave + 8j of the stage (i < NCP):
+  // stage rows 8i + lane/8 (token rows for i < ACP, weight rows after),
+  // physical chunk lane % 8 holding logical chunk (lane % 8) ^ ((row >> 1) & 7).
+  // Byte offsets are 32-bit (the host keeps T*E*2 and 3*E*E*2 below 2^31).
+  uint32_t off[CPW];
+  const uint16_t* cbase[CPW];
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d = t * 32 + 8 * g + 4 * half;
-          const float4 val = make_float4(o[t][4 * g] * inv, o[t][4 * g + 1] * inv, o[t][4 * g + 2] * inv,
-                                         o[t][4 * g + 3] * inv);
-          *reinterpret_cast<float4*>(orow + d) = val;
-        }
-      }
+  for (int j = 0; j < CPW; ++j) {
+    const int i = wave_s + 8 * j;
+    const int row = 8 * i + (lane >> 3);
+    const int lch = (lane & 7) ^ ((row >> 1) & 7);
+    if (i < ACP) {
+      const int t = min(row, T_ - 1);
+      off[j] = static_cast<uint32_t>(t * E + lch * 8) * 2u;
+      cbase[j] = tok;
     } else {
-      const int b = bh / heads;
-      const int h = bh - b * heads;
-      uint16_t* orow = Ocat + (static_cast<size_t>(b) * S + qi) * (heads * D) + h * D;
+      const int r = min(row - AR, WR - 1);
+      const int wrow = (r >> 6) * E + h * D + (r & 63);
+      off[j] = static_cast<uint32_t>(wrow * E + lch * 8) * 2u;
+      cbase[j] = Wqkv_t;
+    }
+  }
+  const bool full_cpw = wave_s + 8 * (CPW - 1) < NCP;  // CPW copies per stage, else CPW - 1
+  const uint32_t lds0 = lds_addr(smem);
+  // Copies j0 .. j1-1 of stage st into ring slot buf.
+  auto issue = [&](int st, int buf, int j0, int j1) {
+    const int k0 = st * 64;
 #pragma unroll
-      for (int t = 0; t < DT; ++t) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int d = t * 32 + 8 * g + 4 * half;
-          u32x2 w;
-          w[0] = pack2<T>(o[t][4 * g] * inv, o[t][4 * g + 1] * inv);
-          w[1] = pack2<T>(o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
-          *reinterpret_cast<u32x2*>(orow + d) = w;
-        }
+    for (int j = 0; j < CPW; ++j) {
+      if (j >= j0 && j < j1 && (j < CPW - 1 || full_cpw)) {
+        load_lds16_sbase(off[j], cbase[j] + k0,
+                         lds0 + 2u * static_cast<uint32_t>(buf * STAGE + (wave_s + 8 * j) * 512));
       }
     }
+  };
+
+  const int lrow = lane & 31;
+  const int lhalf = lane >> 5;
+  // Token rows 32w + lrow and weight rows AR + 32cb + lrow share the swizzle
+  // (lrow >> 1) & 7.
+  const int swz = (lrow >> 1) & 7;
+  floatx16 acc[6];
+#pragma unroll
+  for (int u = 0; u < 6; ++u) {
+    acc[u] = zero16();
+  }
+  // Wave roles (uniform): main waves w < nrb hold K0 K1 V0 V1 in acc[0..3],
+  // Q0 in acc[4] when w is a query block of this part, and Q1 in acc[5] when
+  // it is one past the first nmove; wave 7 holds Q1 of query blocks
+  // qlo .. qlo + nmove - 1 in acc[0..nmove-1].
+  const bool main_w = wave_s < nrb;
+  const bool has_q = main_w && wave_s >= qlo && wave_s < qlo + nq;
+  const bool own_q1 = has_q && wave_s - qlo >= nmove;
+  const bool helper = wave_s == 7;
+
+  // The stage loop; compute(sb, cp) runs this wave's 4 k-steps on the stage
+  // at sb and calls cp(kk) after k-step kk's MFMAs, which issues two of the
+  // copies of stage st + 2 (the last k-step the rest): spread over the stage,
+  // the copies do not queue up behind each other at the address unit while
+  // the MFMAs wait.
+  const int nst = E / 64;
+  auto run = [&](auto compute) {
+    issue(0, 0, 0, CPW);
+    if (nst > 1) {
+      issue(1, 1, 0, CPW);
+    }
+    int buf = 0;   // ring slot of stage st
+    int buf2 = 2;  // ring slot of stage st + 2
+    for (int st = 0; st < nst; ++st) {
+      // This wave's copies of stage st have landed (those of st + 1 may still
+      // be in flight), then everyone's have, and everyone is done with stage
+      // st - 1, whose slot takes stage st + 2.
+      if (st + 1 < nst) {
+        if (full_cpw) {
+          wait_vmcnt<CPW>();
+        } else {
+          wait_vmcnt<CPW - 1>();
+        }
+      } else {
+        wait_vmcnt<0>();
+      }
+      stage_barrier();
+      const bool more = st + 2 < nst;
+      auto cp = [&](int kk) {
+        if (more) {
+          issue(st + 2, buf2, 2 * kk, kk == 3 ? CPW : 2 * kk + 2);
+        }
+      };
+      compute(smem + buf * STAGE, cp);
+      buf = buf == NB - 1 ? 0 : buf + 1;
+      buf2 = buf2 == NB - 1 ? 0 : buf2 + 1;
+    }
+  };
+  auto rd_a = [&](const uint16_t* sb, int kk, int rb) {
+    return *reinterpret_cast<const u32x4*>(sb + (rb * 32 + lrow) * 64 + (((2 * kk + lhalf) ^ swz) << 3));
+  };
+  auto rd_w = [&](const uint16_t* sb, int kk, int cb) {
+    return *reinterpret_cast<const u32x4*>(sb + (AR + cb * 32 + lrow) * 64 + (((2 * kk + lhalf) ^ swz) << 3));
+  };
+  // Main waves: NQ = 0, 1 or 2 Q units.  Fragment slots: [0] tokens, [1..4]
+  // K0 K1 V0 V1 weights, [5..] Q0 Q1 weights.
+  auto main_stage = [&](auto nq_c) {
+    constexpr int NQ = decltype(nq_c)::value;
+    constexpr int NF = 5 + NQ;
+    return [&](const uint16_t* sb, auto cp) {
+      u32x4 f[2][NF];
+      auto rd = [&](int kk, u32x4 (&g)[NF]) {
+        g[0] = rd_a(sb, kk, wave_s);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          g[1 + u] = rd_w(sb, kk, 2 + u);
+        }
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+          g[5 + u] = rd_w(sb, kk, u);
+        }
+      };
+      rd(0, f[0]);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        if (kk < 3) {
+          rd(kk + 1, f[(kk + 1) & 1]);
+        }
+        const u32x4(&g)[NF] = f[kk & 1];
+        acc[0] = mfma32x32x16<T>(g[1], g[0], acc[0]);  // K rows d 0..31
+        acc[1] = mfma32x32x16<T>(g[2], g[0], acc[1]);  // K rows d 32..63
+        acc[2] = mfma32x32x16<T>(g[0], g[3], acc[2]);  // V columns d 0..31
+        acc[3] = mfma32x32x16<T>(g[0], g[4], acc[3]);  // V columns d 32..63
+#pragma unroll
+        for (int u = 0; u < NQ; ++u) {
+          acc[4 + u] = mfma32x32x16<T>(g[5 + u], g[0], acc[4 + u]);  // Q rows d 32u..
+        }
+        cp(kk);
+      }
+    };
+  };
+  // Wave 7: Q1 of NM query blocks.  Fragment slots: [0] Q1 weights, [1..NM]
+  // tokens of blocks qlo ...
+  auto helper_stage = [&](auto nm_c) {
+    constexpr int NM = decltype(nm_c)::value;
+    return [&](const uint16_t* sb, auto cp) {
+      u32x4 f[2][1 + NM];
+      auto rd = [&](int kk, u32x4 (&g)[1 + NM]) {
+        g[0] = rd_w(sb, kk, 1);
+#pragma unroll
+        for (int u = 0; u < NM; ++u) {
+          g[1 + u] = rd_a(sb, kk, qlo + u);
+        }
+      };
+      rd(0, f[0]);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        if (kk < 3) {
+          rd(kk + 1, f[(kk + 1) & 1]);
+        }
+        const u32x4(&g)[1 + NM] = f[kk & 1];
+#pragma unroll
+        for (int u = 0; u < NM; ++u) {
+          acc[u] = mfma32x32x16<T>(g[0], g[1 + u], acc[u]);
+        }
+        cp(kk);
+      }
+    };
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  if (main_w) {
+    if (!has_q) {
+      run(main_stage(I0{}));
+    } else if (!own_q1) {
+      run(main_stage(I1{}));
+    } else {
+      run(main_stage(I2{}));
+    }
+  } else if (helper) {
+    if (nmove == 1) {
+      run(helper_stage(I1{}));
+    } else if (nmove == 2) {
+      run(helper_stage(I2{}));
+    } else {
+      run(helper_stage(I3{}));
+    }
+  } else {
+    run([](const uint16_t*, auto cp) {
+      cp(0);
+      cp(1);
+      cp(2);
+      cp(3);
+    });
+  }
+  __syncthreads();  // every wave is done with the projection buffers
+
+  // Q, K and V^T to LDS.  In a W . tokens^T unit, register 4g + i of lane l
+  // holds d = 32cb + 8g + 4(l/32) + i of token 32rb + l%32; in a tokens . W^T
+  // unit, token 32rb + 8g + 4(l/32) + i and d = 32cb + l%32.
+  uint16_t* Qs = smem;
+  uint16_t* Ks = smem + KOFF;
+  uint16_t* Vs = smem + VOFF;
+  auto store_q = [&](const floatx16& a, int rb, int cb) {
+    const int t = rb * 32 + lrow;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = cb * 32 + 8 * g + 4 * lhalf;
+      u32x2 v;
+      v[0] = pack2<T>(a[4 * g], a[4 * g + 1]);
+      v[1] = pack2<T>(a[4 * g + 2], a[4 * g + 3]);
+      *reinterpret_cast<u32x2*>(Qs + (t - qlo * 32) * D + d0) = v;
+    }
+  };
+  if (main_w) {
+    const int t = wave_s * 32 + lrow;
+    const int r = t & (KT - 1);
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = cb * 32 + 8 * g + 4 * lhalf;
+        u32x2 v;
+        v[0] = pack2<T>(acc[cb][4 * g], acc[cb][4 * g + 1]);
+        v[1] = pack2<T>(acc[cb][4 * g + 2], acc[cb][4 * g + 3]);
+        *reinterpret_cast<u32x2*>(Ks + (t / KT) * TILE + r * D + (((d0 >> 3) ^ ((r >> 1) & 7)) << 3) + (d0 & 7)) = v;
+      }
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int d = cb * 32 + lrow;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int t0 = wave_s * 32 + 8 * g + 4 * lhalf;  // keys t0 .. t0 + 3
+        const int r0 = t0 & (KT - 1);
+        u32x2 v;
+        v[0] = pack2<T>(acc[2 + cb][4 * g], acc[2 + cb][4 * g + 1]);
+        v[1] = pack2<T>(acc[2 + cb][4 * g + 2], acc[2 + cb][4 * g + 3]);
+        uint16_t* vdst = Vs + (t0 / KT) * TILE + d * KT + (((r0 >> 3) ^ ((d >> 1) & 7)) << 3) + (r0 & 7);
+        *reinterpret_cast<u32x2*>(vdst) = v;
+      }
+    }
+    if (has_q) {
+      store_q(acc[4], wave_s, 0);
+      if (own_q1) {
+        store_q(acc[5], wave_s, 1);
+      }
+    }
+  } else if (helper) {
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+      if (u < nmove) {
+        store_q(acc[u], qlo + u, 1);
+      }
+    }
+    if (nrb & 1) {
+      // Keys 32 nrb .. 32 nrb + 31 (the second half of the last key tile):
+      // zeros (masked keys, whose V rows must stay finite).  K rows 32..63 of
+      // that tile are contiguous; V^T rows d hold them in logical chunks 4..7.
+      const int tl = nrb >> 1;
+      const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int c = lane + 64 * q;  // 0..255
+        *reinterpret_cast<u32x4*>(Ks + tl * TILE + 32 * D + 8 * c) = z;
+        const int d = c >> 2;
+        const int lc = 4 + (c & 3);
+        *reinterpret_cast<u32x4*>(Vs + tl * TILE + d * KT + ((lc ^ ((d >> 1) & 7)) << 3)) = z;
+      }
+    }
+  }
+  __syncthreads();
+
+  if (wave < nq) {
+    const int q0 = (qlo + wave) * 32;
+    HalfAttnWave<T, D> w;
+    w.init(Qs + (wave * 32 + lrow) * D, q0, T_, 0, scale, lane);
+    const int nt = (T_ + KT - 1) / KT;
+    floatx16 s_a[2];
+    floatx16 s_b[2];
+    w.qk(Ks, s_a);
+    // Every tile is resident: no loads or barriers between tiles.  Past the
+    // last tile the next tile's scores come from the last K tile and go
+    // unused.
+    for (int j = 0; j < nt; j += 2) {
+      w.step(j, Ks + min(j + 1, nt - 1) * TILE, Vs + j * TILE, s_a, s_b);
+      if (j + 1 < nt) {
+        w.step(j + 1, Ks + min(j + 2, nt - 1) * TILE, Vs + (j + 1) * TILE, s_b, s_a);
+      }
+    }
+    w.store(nullptr, Ocat, bh, H);
   }
 }
 
@@ -1692,6 +2091,30 @@ hipError_t mseLossF32(const float* out, const float* target, size_t n, float nor
     return hipErrorInvalidValue;
   }
   hipLaunchKernelGGL(mse_loss_kernel, dim3(1), dim3(1024), 0, stream, out, target, n, norm, loss);
+  return hipGetLastError();
+}
+
+bool vitQkvAttentionFits(int T_, int E, int H) {
+  return H > 0 && E % H == 0 && E / H == 64 && T_ > 0 && T_ <= 224 && E % 64 == 0 &&
+         static_cast<long long>(T_) * E * 2 < (1LL << 31) && 3LL * E * E * 2 < (1LL << 31);
+}
+
+hipError_t vitQkvAttention(const uint16_t* tokens, const uint16_t* Wqkv_t, uint16_t* out_heads_concat, int B,
+                           int T_, int E, int H, Half t, hipStream_t stream) {
+  if (B <= 0 || !vitQkvAttentionFits(T_, E, H)) {
+    return hipErrorInvalidValue;
+  }
+  const float scale = 1.0f / sqrtf(64.0f);
+  // Two workgroups per (image, head) once there are two query blocks.
+  const int nparts = T_ > 32 ? 2 : 1;
+  const dim3 grid(B * H * nparts);
+  if (t == Half::kBF16) {
+    hipLaunchKernelGGL((vit_qkv_attn_kernel<BF16>), grid, dim3(512), 0, stream, tokens, Wqkv_t, out_heads_concat,
+                       T_, E, H, nparts, scale);
+  } else {
+    hipLaunchKernelGGL((vit_qkv_attn_kernel<F16>), grid, dim3(512), 0, stream, tokens, Wqkv_t, out_heads_concat, T_,
+                       E, H, nparts, scale);
+  }
   return hipGetLastError();
 }
 

@@ -198,6 +198,28 @@ def test_vit_block_ring_stage_depth_bitwise(lc, monkeypatch, p, e):
     np.testing.assert_array_equal(deep, shallow)
 
 
+# The fused QKV-projection + attention kernel (default where head dim is 64
+# and T <= 224) against the separate QKV GEMM and attention kernels
+# (CJ_HIP_VIT_FUSED=0): the projection accumulates in the same k order and the
+# attention runs the same per-wave arithmetic, so the bits match.  T = 25, 9
+# and 169 are not multiples of 4 or 64; T = 196 is config 4's.
+@pytest.mark.parametrize("bn,img,p,e,heads,dtype", [
+    (2, 64, 16, 128, 2, "f16"),    # T = 16
+    (3, 40, 8, 128, 2, "f16"),     # T = 25
+    (5, 96, 16, 192, 3, "bf16"),   # T = 36
+    (1, 48, 16, 128, 2, "bf16"),   # T = 9
+    (1, 208, 16, 128, 2, "f16"),   # T = 169
+    (2, 224, 16, 768, 12, "bf16"),  # config 4's image and width, T = 196
+])
+def test_vit_block_fused_matches_unfused(lc, monkeypatch, bn, img, p, e, heads, dtype):
+    note(f"[case] vit fused vs unfused bn={bn} img={img} p={p} e={e} heads={heads} {dtype}")
+    x, w_conv, w_qkv, w_o = _vit_inputs(bn, 3, img, p, e)
+    fused = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype=dtype)
+    monkeypatch.setenv("CJ_HIP_VIT_FUSED", "0")
+    unfused = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype=dtype)
+    np.testing.assert_array_equal(fused, unfused)
+
+
 def test_vit_block_config4(lc, oracle):
     bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12
     note("[case] config 4 ViT block")
