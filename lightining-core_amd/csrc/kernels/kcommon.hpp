@@ -62,10 +62,19 @@ __device__ __forceinline__ uint32_t pack2<BF16>(float lo, float hi) {
   v[1] = static_cast<__bf16>(hi);
   return __builtin_bit_cast(uint32_t, v);
 }
+// One v_cvt_pk_f16_f32 (round to nearest even, as the scalar conversion)
+// instead of two conversions and an OR.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <>
+__device__ __forceinline__ uint32_t pack2<F16>(float lo, float hi) {
+  f16x2 v;
+  v[0] = static_cast<_Float16>(lo);
+  v[1] = static_cast<_Float16>(hi);
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // acc + lo + hi of a packed 16-bit pair, in one fp32 dot-product
 // instruction (v_dot2c_f32_{bf16,f16} against (1, 1)).
-typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 template <typename T>
 __device__ __forceinline__ float add_pair(uint32_t pair, float acc);
 template <>
