@@ -220,6 +220,28 @@ def test_vit_block_fused_matches_unfused(lc, monkeypatch, bn, img, p, e, heads, 
     np.testing.assert_array_equal(fused, unfused)
 
 
+# The fused kernel's edges: one 64-deep k-stage (E = 64, one head) and the
+# largest token count it takes (T = 224 = 14 x 16 patches of a 224 x 256
+# image: seven full query blocks, keys 224..255 padding), each bit-identical to
+# the separate kernels and, for T = 224, against the oracle on the whole block.
+@pytest.mark.parametrize("bn,ih,iw,p,e,heads,dtype", [
+    (2, 32, 32, 8, 64, 1, "f16"),     # T = 16, E = 64
+    (1, 224, 256, 16, 128, 2, "bf16"),  # T = 224
+])
+def test_vit_block_fused_edges(lc, oracle, monkeypatch, bn, ih, iw, p, e, heads, dtype):
+    note(f"[case] vit fused edges bn={bn} {ih}x{iw} p={p} e={e} heads={heads} {dtype}")
+    x = synth.uniform((bn, 3, ih, iw), lo=0.0, hi=1.0, stream=34)
+    w_conv = synth.normal((e, 3, p, p), std=0.02, stream=35)
+    w_qkv = synth.normal((e, 3 * e), std=0.02, stream=36)
+    w_o = synth.normal((e, e), std=0.02, stream=37)
+    fused = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype=dtype)
+    ref = oracle.vit_block(*(synth.round_to(t, dtype) for t in (x, w_conv, w_qkv, w_o)), heads)
+    assert_parity(ref, fused.reshape(ref.shape), dtype, f"vit fused {ih}x{iw} e{e} {dtype}")
+    monkeypatch.setenv("CJ_HIP_VIT_FUSED", "0")
+    unfused = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype=dtype)
+    np.testing.assert_array_equal(fused, unfused)
+
+
 def test_vit_block_config4(lc, oracle):
     bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12
     note("[case] config 4 ViT block")
