@@ -162,6 +162,15 @@ def cpu_threads_used():
     return 1
 
 
+def device_label(info):
+    """The HIP device name, or (where the runtime reports it empty, as in
+    these containers) the properties that identify the part."""
+    if info["name"]:
+        return info["name"]
+    return (f"{info['gcn_arch'].split(':')[0]}, {info['compute_units']} CUs, {info['max_clock_khz'] / 1e3:.0f} MHz "
+            f"max, {info['total_memory_bytes'] / 2**30:.0f} GiB HBM (HIP device name empty)")
+
+
 def host_record():
     """CPU model and thread counts of the host the CPU baseline runs on."""
     model = ""
@@ -606,9 +615,9 @@ def main():
         "data": "synthetic: SplitMix64 N(0,1) rounded to bf16 (RNE), seed 20260401, inputs resident in HBM",
         "config": {"workload": "configs[4]: matmul2d bf16 GEMM M=N=K=8192 (fp32 accumulate, fp32 C), resident "
                                "session (upload once), launch-only, one launch per step",
-                   "parallelism": "single GPU", "device": info["name"], "arch": info["gcn_arch"],
+                   "parallelism": "single GPU", "device": device_label(info), "arch": info["gcn_arch"],
                    "compute_units": info["compute_units"], "max_clock_khz": info["max_clock_khz"],
-                   "host": host_record()},
+                   "hbm_bytes": info["total_memory_bytes"], "host": host_record()},
         "roofline": roofline,
         "cpu_baseline": cpu_obj,
         "per_config": extras,
