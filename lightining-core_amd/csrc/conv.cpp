@@ -10,10 +10,14 @@
 //    as consecutive S*D slices of the flat NCHW output, repeated when short
 //    (QkvPackRepeat :709-729), then single-head attention.  Every stage stays
 //    in device memory (the reference round-trips through host vectors).
-//  * The ViT block chains four kernels on one stream with the re-layouts in
-//    the epilogues: implicit-GEMM patch-embed conv (+ReLU) writing tokens
-//    [B*T, E]; QKV GEMM writing head-major Q/K and transposed V; flash
-//    attention writing heads concatenated [B*T, E]; output projection.
+//  * The ViT block chains three kernels on one stream: the patch-embed conv
+//    (+ReLU) as a row-major GEMM on the input stored as patch rows (the
+//    stride-P conv's im2col is a permutation of the image, applied once at
+//    upload) writing tokens [B*T, E]; the QKV projection fused with attention
+//    per (image, head), Q/K/V^T kept in LDS, writing heads concatenated
+//    [B*T, E]; the output projection.  CJ_HIP_VIT_PATCHIFY=0 and
+//    CJ_HIP_VIT_FUSED=0 select the implicit-im2col GEMM and the separate QKV
+//    GEMM (head-major Q/K, transposed V) + attention kernels.
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
@@ -264,6 +268,10 @@ struct lcVitBlockSession {
   std::size_t gh = 0, gw = 0, T = 0, M = 0, Mp = 0, K = 0, Dh = 0, S_pad = 0;
   DeviceBuffer stage, x16, wconv16, wqkv_t16, wo_t16, tokens16, q16, k16, vt16, attn16, out;
   bool has_w = false, has_x = false;
+  // The resident input is stored as patch rows [M][K] (x16 holds the
+  // vitPatchify layout and the patch conv is a row-major GEMM), else as
+  // 16-bit NCHW read by the implicit-im2col GEMM.
+  bool patchify = false;
 };
 
 namespace {
@@ -288,6 +296,13 @@ Status vitValidate(const lcVitBlockConfig& c) {
   return Status::kSuccess;
 }
 
+// The patch rows layout is the default; CJ_HIP_VIT_PATCHIFY=0 keeps the
+// image in NCHW for the implicit-im2col GEMM (A/B runs, tests).
+bool vitPatchifyEnabled() {
+  const char* env = getenv("CJ_HIP_VIT_PATCHIFY");
+  return env == nullptr || std::string(env) != "0";
+}
+
 // The fused QKV + attention kernel is the default where it fits;
 // CJ_HIP_VIT_FUSED=0 selects the separate QKV GEMM and attention kernels.
 bool vitFusedEnabled() {
@@ -304,9 +319,13 @@ Status vitForwardDevice(HipContext* ctx, lcVitBlockSession* s) {
   const int T = static_cast<int>(s->T);
   const int M = static_cast<int>(s->M);
   traceOpDispatch(TraceOp::kConv2dNchw, Device::kHIP, Device::kHIP, false, s->M * c.embed * s->K);
-  hipError_t e = kern::patchEmbedGemm(s->x16.as<uint16_t>(), s->wconv16.as<uint16_t>(), s->tokens16.as<uint16_t>(), B,
-                                      static_cast<int>(c.in_channels), static_cast<int>(c.image_h),
-                                      static_cast<int>(c.image_w), static_cast<int>(c.patch), E, ht, ctx->stream);
+  hipError_t e = s->patchify
+                     ? kern::patchTokensGemm(s->x16.as<uint16_t>(), s->wconv16.as<uint16_t>(), s->tokens16.as<uint16_t>(),
+                                             M, static_cast<int>(s->K), E, ht, ctx->stream)
+                     : kern::patchEmbedGemm(s->x16.as<uint16_t>(), s->wconv16.as<uint16_t>(),
+                                            s->tokens16.as<uint16_t>(), B, static_cast<int>(c.in_channels),
+                                            static_cast<int>(c.image_h), static_cast<int>(c.image_w),
+                                            static_cast<int>(c.patch), E, ht, ctx->stream);
   if (e != hipSuccess) {
     return failHip(e, "vit patch-embed launch");
   }
@@ -348,6 +367,17 @@ Status vitUploadX(HipContext* ctx, lcVitBlockSession* s, const float* x) {
   const auto& c = s->cfg;
   const std::size_t n = c.batch * c.in_channels * c.image_h * c.image_w;
   LC_TRY(upload(ctx, s->stage.get(), x, n * sizeof(float)));
+  if (s->patchify) {
+    const hipError_t e = kern::vitPatchify(s->stage.as<float>(), s->x16.as<uint16_t>(), static_cast<int>(c.batch),
+                                           static_cast<int>(c.in_channels), static_cast<int>(c.image_h),
+                                           static_cast<int>(c.image_w), static_cast<int>(c.patch),
+                                           halfOf(c.compute_dtype), ctx->stream);
+    if (e != hipSuccess) {
+      return failHip(e, "vit input conversion");
+    }
+    s->has_x = true;
+    return Status::kSuccess;
+  }
   const hipError_t e = kern::convertPad(s->stage.as<float>(), s->x16.as<uint16_t>(), 1,
                                         static_cast<int>(c.batch * c.in_channels * c.image_h),
                                         static_cast<int>(c.image_w), c.image_w,
@@ -623,7 +653,9 @@ lcError_t lcVitBlockSessionCreate(const lcVitBlockConfig* cfg, lcDeviceKind devi
   const std::size_t bh = c.batch * c.heads;
   const std::size_t h2 = sizeof(uint16_t);
   st = s->stage.ensure(std::max({xs, E * s->K, E * 3 * E}) * sizeof(float));
-  if (st == Status::kSuccess) st = s->x16.ensure(xs * h2);
+  s->patchify = vitPatchifyEnabled();
+  // Patch rows: M x K values (<= the image's), rows up to Mp zero.
+  if (st == Status::kSuccess) st = s->x16.ensure(s->patchify ? s->Mp * s->K * h2 : xs * h2, true);
   if (st == Status::kSuccess) st = s->wconv16.ensure(roundUp(E, kern::kHalfGemmBN) * s->K * h2, true);
   if (st == Status::kSuccess) st = s->wqkv_t16.ensure(roundUp(3 * E, kern::kHalfGemmBN) * E * h2, true);
   if (st == Status::kSuccess) st = s->wo_t16.ensure(roundUp(E, kern::kHalfGemmBN) * E * h2, true);

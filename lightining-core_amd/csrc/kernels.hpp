@@ -128,6 +128,9 @@ hipError_t mseLossF32(const float* out, const float* target, size_t n, float nor
 hipError_t convertPad(const float* src, uint16_t* dst, int batch, int rows, int cols, size_t ld_src,
                       int rows_pad, int cols_pad, size_t src_bstride, size_t dst_bstride, Half t,
                       hipStream_t stream);
+// ViT input: fp32 NCHW x -> 16-bit patch rows xp [B*T][C*P*P] (the im2col of
+// the stride-P patch conv, a permutation of the image); P % 8 == 0, W % 8 == 0.
+hipError_t vitPatchify(const float* x, uint16_t* xp, int B, int C, int H, int W, int P, Half t, hipStream_t stream);
 // dst[b][c][r] = half(src[b][r][c]) (transpose), zero padding to
 // cols_pad x rows_pad.
 hipError_t convertTransposePad(const float* src, uint16_t* dst, int batch, int rows, int cols, size_t ld_src,
@@ -175,6 +178,10 @@ hipError_t gemmHalfTNHalfOut(const uint16_t* A, const uint16_t* Bt, uint16_t* C,
 // [roundup(B*T, 256), E].  Requires P % 8 == 0 and (C*P*P) % 64 == 0.
 hipError_t patchEmbedGemm(const uint16_t* x, const uint16_t* Wt, uint16_t* tokens, int B, int C, int H, int W, int P,
                           int E, Half t, hipStream_t stream);
+// The patch-embed conv as a row-major GEMM on vitPatchify's xp [M][K]:
+// tokens = relu(xp . Wt^T), the same tiles and k order as patchEmbedGemm.
+hipError_t patchTokensGemm(const uint16_t* xp, const uint16_t* Wt, uint16_t* tokens, int M, int K, int E, Half t,
+                           hipStream_t stream);
 // QKV projection for the ViT block: qkv = tokens[M, E] . Wqkv_t[3E, E]^T with
 // the epilogue writing head-major Q, K [B*H, S_pad, Dh] and V transposed
 // Vt [B*H, Dh, S_pad] (16-bit), M = B*T, S = T.

@@ -8,6 +8,42 @@
 
 namespace lchip::k {
 
+// ViT input: fp32 NCHW images -> 16-bit patch rows, xp[b*T + py*gw + px]
+// [c*P*P + ky*P + kx] = x[b][c][py*P + ky][px*P + kx].  The im2col of an
+// unpadded P x P conv with stride P is a permutation of the image, so the
+// patch-embed conv becomes a row-major GEMM on xp.  One thread converts 8
+// consecutive kx (two float4 loads, one 16-byte store); P % 8 == 0 and
+// W % 8 == 0 keep every access aligned.
+template <typename T>
+__global__ __launch_bounds__(256) void patchify_kernel(const float* __restrict__ x, uint16_t* __restrict__ xp, int C,
+                                                       int H, int W, int P, int gw, int T_, long long total8) {
+  const long long i = static_cast<long long>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total8) {
+    return;
+  }
+  const int K = C * P * P;
+  const int k8 = K / 8;
+  const long long m = i / k8;
+  const int k = static_cast<int>(i - m * k8) * 8;
+  const int b = static_cast<int>(m / T_);
+  const int t = static_cast<int>(m - static_cast<long long>(b) * T_);
+  const int py = t / gw;
+  const int px = t - py * gw;
+  const int c = k / (P * P);
+  const int r = k - c * P * P;
+  const int ky = r / P;
+  const int kx = r - ky * P;
+  const float* src = x + ((static_cast<size_t>(b) * C + c) * H + py * P + ky) * W + px * P + kx;
+  const float4 lo = *reinterpret_cast<const float4*>(src);
+  const float4 hi = *reinterpret_cast<const float4*>(src + 4);
+  u32x4 o;
+  o[0] = pack2<T>(lo.x, lo.y);
+  o[1] = pack2<T>(lo.z, lo.w);
+  o[2] = pack2<T>(hi.x, hi.y);
+  o[3] = pack2<T>(hi.z, hi.w);
+  *reinterpret_cast<u32x4*>(xp + m * K + k) = o;
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void convert_pad_kernel(const float* __restrict__ src, uint16_t* __restrict__ dst,
                                                           int rows, int cols, size_t ld_src, int rows_pad,
@@ -190,6 +226,23 @@ hipError_t convertPad(const float* src, uint16_t* dst, int batch, int rows, int 
   } else {
     hipLaunchKernelGGL((convert_pad_kernel<F16>), grid, dim3(256), 0, stream, src, dst, rows, cols, ld_src, rows_pad,
                        cols_pad, src_bstride, dst_bstride);
+  }
+  return hipGetLastError();
+}
+
+hipError_t vitPatchify(const float* x, uint16_t* xp, int B, int C, int H, int W, int P, Half t, hipStream_t stream) {
+  if (B <= 0 || C <= 0 || P <= 0 || P % 8 != 0 || W % 8 != 0 || H < P || W < P) {
+    return hipErrorInvalidValue;
+  }
+  const int gh = H / P;
+  const int gw = W / P;
+  const int T_ = gh * gw;
+  const long long total8 = static_cast<long long>(B) * T_ * C * P * P / 8;
+  const dim3 grid(static_cast<unsigned>((total8 + 255) / 256));
+  if (t == Half::kBF16) {
+    hipLaunchKernelGGL((patchify_kernel<BF16>), grid, dim3(256), 0, stream, x, xp, C, H, W, P, gw, T_, total8);
+  } else {
+    hipLaunchKernelGGL((patchify_kernel<F16>), grid, dim3(256), 0, stream, x, xp, C, H, W, P, gw, T_, total8);
   }
   return hipGetLastError();
 }

@@ -2347,6 +2347,31 @@ hipError_t patchEmbedGemm(const uint16_t* x, const uint16_t* Wt, uint16_t* token
   return launch_gemm_half<F16>(la, Wt, M, E, K, K, EpiHalf<F16>{tokens, E, 1}, stream);
 }
 
+hipError_t patchTokensGemm(const uint16_t* xp, const uint16_t* Wt, uint16_t* tokens, int M, int K, int E, Half t,
+                           hipStream_t stream) {
+  if (K % kHBK != 0) {
+    return hipErrorInvalidValue;
+  }
+  if (vit_ring_enabled() && ring_fits(128, K)) {
+    const RingRowMajor ra{xp, K};
+    if (vit_ring_bk128(K)) {
+      if (t == Half::kBF16) {
+        return launch_gemm_ring<BF16, 128, 64, 4, 2, 3, 128>(ra, Wt, M, E, K, K, EpiHalf<BF16>{tokens, E, 1}, stream);
+      }
+      return launch_gemm_ring<F16, 128, 64, 4, 2, 3, 128>(ra, Wt, M, E, K, K, EpiHalf<F16>{tokens, E, 1}, stream);
+    }
+    if (t == Half::kBF16) {
+      return launch_gemm_ring<BF16, 128, 64, 4, 2, 4>(ra, Wt, M, E, K, K, EpiHalf<BF16>{tokens, E, 1}, stream);
+    }
+    return launch_gemm_ring<F16, 128, 64, 4, 2, 4>(ra, Wt, M, E, K, K, EpiHalf<F16>{tokens, E, 1}, stream);
+  }
+  const LoadRowMajor la{xp, K};
+  if (t == Half::kBF16) {
+    return launch_gemm_half<BF16>(la, Wt, M, E, K, K, EpiHalf<BF16>{tokens, E, 1}, stream);
+  }
+  return launch_gemm_half<F16>(la, Wt, M, E, K, K, EpiHalf<F16>{tokens, E, 1}, stream);
+}
+
 hipError_t qkvProjectGemm(const uint16_t* tokens, const uint16_t* Wqkv_t, uint16_t* q, uint16_t* k, uint16_t* vt,
                           int B, int T_, int E, int H, int S_pad, Half t, hipStream_t stream) {
   const int M = B * T_;

@@ -242,6 +242,29 @@ def test_vit_block_fused_edges(lc, oracle, monkeypatch, bn, ih, iw, p, e, heads,
     np.testing.assert_array_equal(fused, unfused)
 
 
+# The input stored as patch rows with the patch conv as a row-major GEMM (the
+# default) against the implicit-im2col GEMM on the NCHW image
+# (CJ_HIP_VIT_PATCHIFY=0): same tiles and k order, so the same bits.  Shapes:
+# P = 8, 16 and 32, an image that is not a multiple of the patch (the last
+# 8 columns and rows are not covered), non-square.
+@pytest.mark.parametrize("bn,ih,iw,p,e,heads,dtype", [
+    (2, 64, 64, 16, 128, 2, "f16"),
+    (3, 40, 48, 8, 128, 2, "bf16"),
+    (2, 64, 64, 32, 256, 2, "f16"),
+    (1, 56, 40, 16, 128, 1, "bf16"),
+])
+def test_vit_block_patch_rows_bitwise(lc, monkeypatch, bn, ih, iw, p, e, heads, dtype):
+    note(f"[case] vit patch rows bn={bn} {ih}x{iw} p={p} e={e} heads={heads} {dtype}")
+    x = synth.uniform((bn, 3, ih, iw), lo=0.0, hi=1.0, stream=38)
+    w_conv = synth.normal((e, 3, p, p), std=0.02, stream=39)
+    w_qkv = synth.normal((e, 3 * e), std=0.02, stream=40)
+    w_o = synth.normal((e, e), std=0.02, stream=41)
+    rows = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype=dtype)
+    monkeypatch.setenv("CJ_HIP_VIT_PATCHIFY", "0")
+    nchw = lc.vit_block(x, w_conv, w_qkv, w_o, heads, compute_dtype=dtype)
+    np.testing.assert_array_equal(rows, nchw)
+
+
 def test_vit_block_config4(lc, oracle):
     bn, c, img, p, e, heads = 8, 3, 224, 16, 768, 12
     note("[case] config 4 ViT block")
