@@ -699,19 +699,34 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_q16_kernel(Src src, floa
     }
   }
   __syncthreads();
+  // The merge factors exp2(m_w - m_all), once per (query, wave) pair, into
+  // the unused tail of wave 0's region (past its parked O).
+  constexpr int FOFF = (32 + 16 * PS + 3) & ~3;
+  static_assert(FOFF + 16 * (KS + 1) <= KVF, "merge factors fit");
+  float* fw = &kv[0][FOFF];
+  if (threadIdx.x < 16 * KS) {
+    const int q = threadIdx.x & 15;
+    const int w = threadIdx.x >> 4;
+    float mq = kMaskValue;
+#pragma unroll
+    for (int u = 0; u < KS; ++u) {
+      mq = fmaxf(mq, kv[u][q]);
+    }
+    fw[16 + w * 16 + q] = exp2f(kv[w][q] - mq);
+    if (w == 0) {
+      fw[q] = mq;
+    }
+  }
+  __syncthreads();
   // Thread (query ql, slot) merges output columns d = slot, slot + 4 KS, ...
   const int ql = threadIdx.x & 15;
   const int slot = threadIdx.x >> 4;
-  float m_all = kMaskValue;
-#pragma unroll
-  for (int w = 0; w < KS; ++w) {
-    m_all = fmaxf(m_all, kv[w][ql]);
-  }
+  const float m_all = fw[ql];
   float f[KS];
   float l_all = 0.0f;
 #pragma unroll
   for (int w = 0; w < KS; ++w) {
-    f[w] = exp2f(kv[w][ql] - m_all);
+    f[w] = fw[16 + w * 16 + ql];
     l_all += f[w] * kv[w][16 + ql];
   }
   const float inv = 1.0f / l_all;
