@@ -312,6 +312,15 @@ lcError_t lcAttentionSessionTrainStepWithPolicy(lcAttentionSession* session, con
                                                 float* v, const float* target, float* out, float learning_rate,
                                                 float* loss_out, const lcAttentionIoPolicy* policy);
 
+/* Launch-only repeat of the session's resident train step (no uploads, no
+ * downloads, no loss; V updated in place on the device each step), then a
+ * stream synchronisation.  The loop of the reference's training benchmark on
+ * its resident fast path (benchmarks/bench_attention.cpp:248-269, which calls
+ * AttentionSession::trainStep per step), run in C; the train-step analogue of
+ * lcAttentionSessionRunCached.  Needs q, k, v and target resident (a step that
+ * uploaded them); learning_rate <= 0 -> LC_INVALID_VALUE. */
+lcError_t lcAttentionSessionTrainRunCached(lcAttentionSession* session, float learning_rate, size_t repeat_count);
+
 /* --- matmul ------------------------------------------------------------------ */
 
 /* MatMulIoPolicy (reference include/lightning_core/core/ops/policy.hpp:8-13). */

@@ -714,6 +714,34 @@ lcError_t lcAttentionSessionTrainStepWithPolicy(lcAttentionSession* session, con
   return LC_SUCCESS;
 }
 
+lcError_t lcAttentionSessionTrainRunCached(lcAttentionSession* session, float learning_rate, size_t repeat_count) {
+  if (session == nullptr || repeat_count == 0 || !(learning_rate > 0.0f)) {
+    return toLc(fail(Status::kInvalidValue, "attention session: null session, zero repeat or learning_rate <= 0"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(session->device, "attention session train step", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  lcAttentionIoPolicy p = session->default_policy;
+  p.upload_q = p.upload_k = p.upload_v = p.upload_target = 0;
+  p.download_out = p.download_v = 0;
+  p.synchronize = 0;
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  // Resident tensors only: nothing is uploaded or downloaded, so the host
+  // pointers the step's argument checks require are never read or written.
+  float unused = 0.0f;
+  for (std::size_t i = 0; i < repeat_count; ++i) {
+    st = attentionTrainResident(ctx, session->res, session->shape, &unused, &unused, &unused, &unused, &unused,
+                                learning_rate, nullptr, p);
+    if (st != Status::kSuccess) {
+      return toLc(st);
+    }
+    ++session->train_step_count;
+  }
+  return toLc(syncStream(ctx));
+}
+
 lcError_t lcAttentionSessionTrainStep(lcAttentionSession* session, const float* q, const float* k, float* v,
                                       const float* target, float* out, float learning_rate, float* loss_out) {
   if (session == nullptr) {

@@ -257,6 +257,12 @@ class AttentionSession:
         """Launch-only repeat over the resident inputs, then synchronise."""
         _check(self._invoke("lcAttentionSessionRunCached", repeat_count))
 
+    def train_run_cached(self, learning_rate: float, repeat_count: int = 1):
+        """repeat_count resident train steps in C (no uploads, downloads or
+        loss; V updated on the device), then synchronise: the loop of the
+        reference's training benchmark (bench_attention.cpp:248-269)."""
+        _check(self._invoke("lcAttentionSessionTrainRunCached", float(learning_rate), repeat_count))
+
     def _train_args(self, q, k, v, target):
         q, k, v = self._args(q, k, v)
         target = _f32(target)

@@ -177,6 +177,7 @@ SIGNATURES = {
     "lcAttentionSessionForward": (_E, [c_void_p, BUF, BUF, BUF, BUF]),
     "lcAttentionSessionForwardWithPolicy": (_E, [c_void_p, BUF, BUF, BUF, BUF, P(AttentionIoPolicyC)]),
     "lcAttentionSessionRunCached": (_E, [c_void_p, c_size]),
+    "lcAttentionSessionTrainRunCached": (_E, [c_void_p, c_float, c_size]),
     "lcAttentionTrainStep": (_E, [BUF, BUF, BUF, BUF, BUF, c_float, P(AttentionConfig), c_int, BUF]),
     "lcAttentionTrainStepWithPolicy": (_E, [BUF, BUF, BUF, BUF, BUF, c_float, P(AttentionConfig), c_int, BUF,
                                             P(AttentionIoPolicyC)]),

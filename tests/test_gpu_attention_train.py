@@ -91,6 +91,38 @@ def test_train_steps_on_resident_v(lc, oracle):
     sess.close()
 
 
+@pytest.mark.parametrize("s,d,causal", [(256, 64, False), (100, 48, True)])
+def test_train_run_cached_matches_steps(lc, s, d, causal):
+    # train_run_cached(lr, n) (the C loop of resident steps) leaves the same V
+    # as n resident train_step_with_policy calls: same kernels, same order.
+    q, k, v, t = (synth.normal((s, d), stream=700 + i) for i in range(4))
+    lr = 0.5
+    up = lc.AttentionIoPolicy(download_out=False, download_v=False, synchronize=True)
+    keep = lc.AttentionIoPolicy(upload_q=False, upload_k=False, upload_v=False, upload_target=False,
+                                download_out=False, download_v=False, synchronize=False)
+    get_v = lc.AttentionIoPolicy(upload_q=False, upload_k=False, upload_v=False, upload_target=False,
+                                 download_out=True, download_v=True, synchronize=True)
+    a = lc.AttentionSession(s, d, causal=causal)
+    b = lc.AttentionSession(s, d, causal=causal)
+    for sess in (a, b):
+        sess.train_step_with_policy(q, k, v, t, lr, up)
+    for _ in range(5):
+        a.train_step_with_policy(q, k, v, t, lr, keep)
+    b.train_run_cached(lr, 5)
+    out_a, va, _ = a.train_step_with_policy(q, k, v.copy(), t, lr, get_v)
+    out_b, vb, _ = b.train_step_with_policy(q, k, v.copy(), t, lr, get_v)
+    np.testing.assert_array_equal(va, vb)
+    np.testing.assert_array_equal(out_a, out_b)
+    assert not np.array_equal(va, v)
+    with pytest.raises(RuntimeError, match="invalid value"):
+        b.train_run_cached(0.0, 1)
+    fresh = lc.AttentionSession(s, d, causal=causal)
+    with pytest.raises(RuntimeError, match="no resident input"):
+        fresh.train_run_cached(lr, 1)
+    for sess in (a, b, fresh):
+        sess.close()
+
+
 def test_loss_every_sampling(lc):
     # loss_every = 3: steps 0, 3, 6 measure the loss, the others repeat the
     # last measured value (src/attention.cpp:309-336)

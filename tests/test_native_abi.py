@@ -131,6 +131,7 @@ def test_validation_before_device_work():
     assert lib.lcMatMul(fp, fp, out.ctypes.data_as(N.FP), 0, 3, 2, N.LC_DEVICE_HIP) == N.LC_INVALID_VALUE
     cfg = N.AttentionConfig(0, 2, 0)
     assert lib.lcAttentionForward(fp, fp, fp, fp, ctypes.byref(cfg), N.LC_DEVICE_HIP) == N.LC_INVALID_VALUE
+    assert lib.lcAttentionSessionTrainRunCached(None, 0.5, 1) == N.LC_INVALID_VALUE
     # non-hip devices are served elsewhere: not supported, never a CPU fallback
     assert lib.lcMatMul(fp, fp, out.ctypes.data_as(N.FP), 2, 3, 2, N.LC_DEVICE_CPU) == N.LC_NOT_SUPPORTED
     assert lib.lcMatMul(fp, fp, out.ctypes.data_as(N.FP), 2, 3, 2, 7) == N.LC_INVALID_VALUE
