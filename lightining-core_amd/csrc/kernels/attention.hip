@@ -1534,7 +1534,7 @@ template <typename T>
 __global__ __launch_bounds__(512) void vit_qkv_attn_kernel(const uint16_t* __restrict__ tokens,
                                                           const uint16_t* __restrict__ Wqkv_t,
                                                           uint16_t* __restrict__ Ocat, int T_, int E, int H,
-                                                          int nparts, float scale) {
+                                                          int nparts, int tb, int th, float scale) {
   constexpr int D = 64;
   constexpr int KT = 64;
   constexpr int TILE = KT * D;            // elements of a K (or V^T) tile
@@ -1559,10 +1559,28 @@ __global__ __launch_bounds__(512) void vit_qkv_attn_kernel(const uint16_t* __res
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wave_s = __builtin_amdgcn_readfirstlane(wave);
-  const int bh = blockIdx.x / nparts;
-  const int part = blockIdx.x - bh * nparts;
-  const int b = bh / H;
-  const int h = bh - b * H;
+  // Workgroup -> (image, head, part).  With tb > 0 the 8 XCDs (workgroup w
+  // runs on XCD w % 8) each take a tb x th block of (image, head) pairs, so
+  // an XCD's L2 fetches the tokens of tb images and the weights of th heads
+  // (the host picks the block that minimises those bytes); else in order.
+  int b;
+  int h;
+  int part;
+  if (tb > 0) {
+    const int x = blockIdx.x & 7;
+    const int l = blockIdx.x >> 3;
+    const int tiles_b = static_cast<int>(gridDim.x) / (H * nparts) / tb;
+    part = l % nparts;
+    const int r = l / nparts;
+    b = (x % tiles_b) * tb + r % tb;
+    h = (x / tiles_b) * th + r / tb;
+  } else {
+    const int q = blockIdx.x / nparts;
+    part = blockIdx.x - q * nparts;
+    b = q / H;
+    h = q - b * H;
+  }
+  const int bh = b * H + h;
   const uint16_t* tok = tokens + static_cast<size_t>(b) * T_ * E;
   const int nrb = (T_ + 31) >> 5;
   const int per = (nrb + nparts - 1) / nparts;
@@ -2123,12 +2141,35 @@ hipError_t vitQkvAttention(const uint16_t* tokens, const uint16_t* Wqkv_t, uint1
   // Two workgroups per (image, head) once there are two query blocks.
   const int nparts = T_ > 32 ? 2 : 1;
   const dim3 grid(B * H * nparts);
+  // XCD blocks: tb images x th heads per XCD, tb | B, th | H, 8 blocks;
+  // per XCD the L2 misses the tokens of tb images (T rows) and the weights
+  // of th heads (192 rows), so minimise tb * T + th * 192.
+  int tb = 0;
+  int th = 0;
+  if ((B * H) % 8 == 0) {
+    long long best = -1;
+    for (int cb = 1; cb <= B; ++cb) {
+      if (B % cb != 0 || (B * H / 8) % cb != 0) {
+        continue;
+      }
+      const int ch = B * H / 8 / cb;
+      if (H % ch != 0) {
+        continue;
+      }
+      const long long cost = static_cast<long long>(cb) * T_ + 192LL * ch;
+      if (best < 0 || cost < best) {
+        best = cost;
+        tb = cb;
+        th = ch;
+      }
+    }
+  }
   if (t == Half::kBF16) {
     hipLaunchKernelGGL((vit_qkv_attn_kernel<BF16>), grid, dim3(512), 0, stream, tokens, Wqkv_t, out_heads_concat,
-                       T_, E, H, nparts, scale);
+                       T_, E, H, nparts, tb, th, scale);
   } else {
     hipLaunchKernelGGL((vit_qkv_attn_kernel<F16>), grid, dim3(512), 0, stream, tokens, Wqkv_t, out_heads_concat, T_,
-                       E, H, nparts, scale);
+                       E, H, nparts, tb, th, scale);
   }
   return hipGetLastError();
 }
