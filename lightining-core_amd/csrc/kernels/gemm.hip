@@ -494,7 +494,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_kernel(LoadA load_a,
 // 16-byte chunks are XOR-swizzled by (row & 15), so the 16 rows of an MFMA
 // fragment read sit in distinct LDS banks.  Two stages: block b+1 loads
 // while block b is multiplied (v_mfma_f32_16x16x32, the W waves taking the
-// block's 32-wide k-steps in turn).  The W partial tiles are summed through
+// block's 32-wide k-steps in turn).  With KS == 1 workgroup ct walks its
+// k-blocks starting at block (5 * ct) % nkb and wrapping around: workgroups
+// that run together then read different 512-byte column slabs of their rows
+// instead of the same slab 16 KB apart in every row, which spreads their
+// reads over the HBM channels (16x8192x8192: 23.9 -> 21.3 us at 128
+// workgroups).  The W partial tiles are summed through
 // LDS (over the stages, all reads done).  With KS > 1 each workgroup stores
 // its partial to the workspace with device-scope stores, waits for them,
 // and bumps its column tile's counter; the one that brings it to KS sums the
@@ -575,23 +580,30 @@ __global__ __launch_bounds__(W * 64) void gemm_skinny_kernel(const uint16_t* __r
   }
   const int r16 = lane & 15;
   const int cg = lane >> 4;
+  // The i-th block this workgroup multiplies (i < nb): its range rotated by
+  // rot when unsplit, in k order otherwise.
+  const int nb = kb1 - kb0;
+  const int rot = (KS == 1 && nb > 0) ? (5 * ct) % nb : 0;
+  auto block = [&](int i) {
+    const int q = i + rot;
+    return kb0 + (q >= nb ? q - nb : q);
+  };
 #pragma unroll
   for (int p = 0; p < S - 1; ++p) {
-    if (kb0 + p < kb1) {
-      issue(kb0 + p, p);
+    if (p < nb) {
+      issue(block(p), p);
     }
   }
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int sl = kb - kb0;
-    if (kb + S - 1 < kb1) {
-      issue(kb + S - 1, (sl + S - 1) % S);
-      wait_vmcnt<(S - 1) * PAIRS>();  // this wave's copies of block kb have landed
+  for (int sl = 0; sl < nb; ++sl) {
+    if (sl + S - 1 < nb) {
+      issue(block(sl + S - 1), (sl + S - 1) % S);
+      wait_vmcnt<(S - 1) * PAIRS>();  // this wave's copies of block sl have landed
     } else {
       wait_vmcnt<0>();
     }
     stage_barrier();  // everyone's have
     const uint16_t* st = sm + (sl % S) * STAGE;
-    const int steps = min(KB, K - kb * KB) / 32;
+    const int steps = min(KB, K - block(sl) * KB) / 32;
     for (int s = wave; s < steps; s += W) {
       const int ch = 4 * s + cg;  // logical 16-byte chunk of this lane's 8 k
       const u32x4 a = *reinterpret_cast<const u32x4*>(st + (NR + r16) * KB + ((ch ^ r16) << 3));
@@ -2227,7 +2239,13 @@ GemmHalfVariant gemmHalfChoose(int M, int N) {
 int skinnySplits(int N, int K, int cus) {
   const int tiles = (N + 16 * kSkinnyNT - 1) / (16 * kSkinnyNT);
   const int kblocks = (K + kSkinnyKB - 1) / kSkinnyKB;
-  // Enough workgroups to cover the CUs, at least two k-blocks per split.
+  // Column tiles for half the CUs or more stream Bt as fast as more
+  // workgroups would (16x8192x8192: 128 workgroups unsplit 21.3 us, 256 with
+  // two splits 22.0-22.3 us): no split-K and its partial round trip.  Fewer
+  // tiles split k until the CUs are covered, keeping two k-blocks per split.
+  if (2 * tiles >= std::max(cus, 1)) {
+    return 1;
+  }
   int splits = 1;
   while (splits < kSkinnyMaxSplits && tiles * splits < std::max(cus, 1) && kblocks / (splits * 2) >= 2) {
     splits *= 2;
