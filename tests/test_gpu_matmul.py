@@ -143,6 +143,27 @@ def test_matmul_bf16_skinny_split_k(lc, oracle, m, k, n):
     np.testing.assert_array_equal(again, first)
 
 
+@pytest.mark.parametrize("m,k,n", [(16, 4096, 8192), (7, 1000, 8200), (16, 8192, 8256)])
+def test_matmul_bf16_skinny_unsplit(lc, oracle, m, k, n):
+    """Column tiles for half the CUs or more: no split-K, each workgroup walks
+    its k-blocks from block (5 * tile) mod nkb.  Ragged N (a last column tile
+    past N) and K (a short last k-block that some workgroups read first);
+    repeated launches are bit-identical."""
+    a = synth.normal((m, k), stream=13)
+    b = synth.normal((k, n), stream=14)
+    note(f"[case] skinny unsplit {m}x{k}x{n}")
+    s = lc.MatMulResidentSession(m, k, n, "bf16")
+    s.start_into(a, b)
+    first = s.finish_into().reshape(m, n).copy()
+    a_r, b_r = synth.round_bf16(a), synth.round_bf16(b)
+    cols = np.unique(np.concatenate([np.arange(0, 64), np.linspace(64, n - 65, 24).astype(int), np.arange(n - 64, n)]))
+    ref = oracle.matmul(a_r, np.ascontiguousarray(b_r[:, cols]))
+    assert_parity(ref, first[:, cols], "bf16", f"bf16 skinny unsplit {m}x{k}x{n}")
+    s.run_batch_sync_cached_no_download(3)
+    again = s.finish_into().reshape(m, n)
+    np.testing.assert_array_equal(again, first)
+
+
 def test_resident_session_protocol(lc, oracle):
     m, k, n = 96, 80, 72
     a = synth.uniform((m, k), stream=9)
