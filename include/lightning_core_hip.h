@@ -352,8 +352,11 @@ lcError_t lcMatMulWithPolicyBatched(const float* a, const float* b, float* out, 
 lcError_t lcMatMulResetTuning(void);
 
 /* No counterpart in the reference: for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc).  out = a . b in fp32 with the kernels of lcMatMul, on
+ * memory (tight serving loops, harnesses that forbid hipMalloc).  A
+ * synchronous call on the library's own stream (it clears a failure word with
+ * hipMemsetAsync, copies it back and synchronises before returning), so it
+ * must not be called while a stream capture is active.  out = a . b in fp32
+ * with the kernels of lcMatMul, on
  * device-resident row-major a [m, k], b [k, n], out [m, n]; every other byte
  * the kernels touch (stream-K partial tiles and flags, zero-padded copies of
  * an operand whose dims are not multiples of 64 or whose base is not 16-byte
@@ -383,6 +386,14 @@ lcError_t lcMatMulResidentSessionRunBatchSync(lcMatMulResidentSession* s, const 
 lcError_t lcMatMulResidentSessionRunBatchSyncNoDownload(lcMatMulResidentSession* s, const float* a,
                                                         const float* b, float* out, size_t repeat_count);        /* :1367 */
 lcError_t lcMatMulResidentSessionRunBatchSyncCachedNoDownload(lcMatMulResidentSession* s, size_t repeat_count); /* :1371 */
+/* Measurement helpers, no reference counterpart (the roofline timing of a
+ * single kernel).  TimeLaunches: `count` launch-only GEMMs on the resident
+ * inputs, back to back on the backend stream with a hipEvent pair around each
+ * launch, then a sync; ms_out[i] = launch i's event-measured duration.
+ * KernelName: "<tune-cache variant> <kernel function>" of the GEMM the
+ * session's shape runs (e.g. "half_w4h_256x256 gemm_half_tn_w4h_kernel"). */
+lcError_t lcMatMulResidentSessionTimeLaunches(lcMatMulResidentSession* s, size_t count, float* ms_out);
+lcError_t lcMatMulResidentSessionKernelName(lcMatMulResidentSession* s, char* buf, size_t cap);
 
 /* --- conv2d and the integrated conv -> attention pipeline -------------------- */
 

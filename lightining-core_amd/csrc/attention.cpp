@@ -313,6 +313,8 @@ Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnSh
   }
   if (policy.download_out || policy.synchronize) {
     LC_TRY(syncStream(ctx));
+  } else if (repeat > 0) {
+    LC_TRY(noteEnqueued(ctx, TraceOp::kAttentionForward, repeat));
   }
   return Status::kSuccess;
 }
@@ -398,6 +400,8 @@ Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShap
   }
   if (policy.download_out || policy.download_v || loss_out != nullptr || policy.synchronize) {
     LC_TRY(syncStream(ctx));
+  } else {
+    LC_TRY(noteEnqueued(ctx, TraceOp::kAttentionForward, 1));
   }
   return Status::kSuccess;
 }

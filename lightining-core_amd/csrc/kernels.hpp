@@ -141,13 +141,16 @@ hipError_t convertTransposePad(const float* src, uint16_t* dst, int batch, int r
 // ldb), K a multiple of kHalfGemmBK, A readable up to roundup(M, 256) rows and
 // Bt up to roundup(N, 256) rows.  Variants (block tile, waves): kW4 256x256
 // with 4 waves and a ring of 32-deep k slices, kW4D the same waves over two
-// 64-deep stages, kLds 256x256 with 8 waves, all three with direct
+// 64-deep stages, kW4R / kW4H 4 waves over a ring of 64-deep parts (kW4H:
+// barrier mid-stage, a half stage of fragments in registers, 16x16x32
+// MFMAs), kLds 256x256 with 8 waves, all with direct
 // global->LDS loads; kBig8 / kBig4 256x256 with 8 / 4 waves, kMid 128x128,
 // kSmall 64x64, kSkinny for M <= 16 (split-K when given a SkinnyWork);
 // kAuto follows gemmHalfChoose
-// (CJ_HIP_GEMM_TILE=w4|w4d|lds|big8|big4|mid|small overrides it).
+// (CJ_HIP_GEMM_TILE=w4h|w4r|w4|w4d|lds|big8|big4|mid|small overrides it).
 enum class GemmHalfVariant {
-  kAuto = 0, kLds = 1, kBig8 = 2, kBig4 = 3, kMid = 4, kSmall = 5, kSkinny = 6, kW4 = 7, kW4D = 8, kW4R = 9
+  kAuto = 0, kLds = 1, kBig8 = 2, kBig4 = 3, kMid = 4, kSmall = 5, kSkinny = 6, kW4 = 7, kW4D = 8, kW4R = 9,
+  kW4H = 10
 };
 GemmHalfVariant gemmHalfChoose(int M, int N);
 // Workspace of the skinny GEMM's split-K: partial tiles (max_splits x
@@ -202,7 +205,8 @@ hipError_t attentionHalf(const uint16_t* q, const uint16_t* k, const uint16_t* v
 
 // ViT: QKV projection of each (image, head) fused with its attention
 // (vit_qkv_attn_kernel); tokens [B*T][E], Wqkv_t [3E][E], output
-// heads-concatenated [B*T][E].  Needs E / H == 64, T <= 256, E % 64 == 0.
+// heads-concatenated [B*T][E].  Needs E / H == 64, T <= 224 (the kernel's LDS
+// holds 224 token rows), E % 64 == 0.
 bool vitQkvAttentionFits(int T_, int E, int H);
 hipError_t vitQkvAttention(const uint16_t* tokens, const uint16_t* Wqkv_t, uint16_t* out_heads_concat, int B,
                            int T_, int E, int H, Half t, hipStream_t stream);

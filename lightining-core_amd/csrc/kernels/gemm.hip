@@ -15,6 +15,7 @@
 #include <stdlib.h>
 
 #include <string>
+#include <type_traits>
 
 #include "../kernels.hpp"
 #include "kcommon.hpp"
@@ -506,20 +507,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_tn_kernel(LoadA load_a,
 // KS partials in k order (deterministic), writes C and resets the counter to
 // zero for the next launch.  No workgroup ever waits for another.
 //   16x16x32 layout: A[m = l%16][k = 8(l/16)+j], B[k = 8(l/16)+j][n = l%16],
-//   D[m = 4(l/16) + i][n = l%16], i = 0..3.
+//   D[m = 4(l/16) + i][n = l%16], i = 0..3 (mfma16x16x32, kcommon.hpp).
 // ---------------------------------------------------------------------------
-template <typename T>
-__device__ __forceinline__ floatx4 mfma16x16x32(u32x4 a, u32x4 b, floatx4 c);
-template <>
-__device__ __forceinline__ floatx4 mfma16x16x32<BF16>(u32x4 a, u32x4 b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
-                                                 0, 0);
-}
-template <>
-__device__ __forceinline__ floatx4 mfma16x16x32<F16>(u32x4 a, u32x4 b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-                                                0);
-}
 
 constexpr int kSkinnyNT = 4;     // 16-column tiles per workgroup
 constexpr int kSkinnyWaves = 8;
@@ -1426,6 +1415,219 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4r_kernel(const uint16_t* _
 }
 
 // ---------------------------------------------------------------------------
+// 16-bit TN GEMM, 256x256 tile, 4 waves of 128x128 (one per SIMD), with the
+// fragments of a whole half stage held in registers (the default from 256
+// tiles).  LDS is the ring of ten 16 KiB parts of gemm_half_tn_w4r_kernel
+// (part p = stage p / 4, type p % 4: A rows 0-127, A rows 128-255, Bt rows
+// 0-127, Bt rows 128-255; slot p % 10; 128-byte rows, chunk c of row r at
+// c ^ ((r >> 1) & 7)), but each stage has its one barrier in the middle:
+//   first half of stage s   MFMAs of k 0..31 from registers r0, while the
+//                           fragments of k 32..63 of stage s are read into r1;
+//   barrier                 this wave's copies of stage s + 1 have landed and
+//                           its reads of stage s are done (so stage s retires);
+//   second half             MFMAs of k 32..63 from r1, while k 0..31 of stage
+//                           s + 1 are read into r0.
+// A fragment read thus has half a stage (64 MFMAs) to land, and no MFMA waits
+// on a barrier.  The copies of stage s + 2 go out one per 8 MFMAs over the
+// whole stage: its A parts during the first half into the slots stage s - 1
+// left, its Bt parts after the barrier into stage s's, so every copy has at
+// least a half stage before the barrier that waits for it.
+//
+// v_mfma_f32_16x16x32 (8 x 8 blocks of 16x16 per wave, 64 MFMAs per 32-deep
+// k-step): measured against the same schedule on 32x32x16 at 8192^3, 1463 vs
+// 1386 TFLOP/s on one box; the per-element k order is unchanged (results are
+// bit-identical to the other 256x256 kernels).  Copy j (0..3) of wave w for
+// one part fills part rows 32w + 8j .. + 7: the four copies share one M0 and
+// step by the instruction offset.  The stage bodies are unrolled by five (the
+// ring's period), so every slot is a constant and every fragment read is one
+// ds_read_b128 with an immediate offset from one of six lane bases.
+// Operands padded to 256 rows and K to 64; lane offsets are 32-bit (the host
+// keeps 256 * ld * 2 bytes below 2^31).
+// ---------------------------------------------------------------------------
+template <typename T, typename Epi>
+__global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* __restrict__ A,
+                                                               const uint16_t* __restrict__ Bt, int M, int N, int K,
+                                                               int lda, int ldb, int tiles_n, Epi epi) {
+  constexpr int BM = 256, BN = 256, BK = 64;
+  constexpr int PARTB = 128 * BK * 2;  // bytes per part
+  constexpr int NPART = 10;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[NPART * PARTB / 2];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = (wave >> 1) * 128;
+  const int wn = (wave & 1) * 128;
+
+  constexpr int GROUP = 4;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int nwg = gridDim.x;
+  const int full = nwg & ~7;
+  int pid = blockIdx.x;
+  if (pid < full) {
+    pid = (pid & 7) * (full >> 3) + (pid >> 3);
+  }
+  const int group_size = GROUP * tiles_n;
+  const int group = pid / group_size;
+  const int first_m = group * GROUP;
+  const int gm = min(tiles_m - first_m, GROUP);
+  const int in_group = pid - group * group_size;
+  const int bm = (first_m + in_group % gm) * BM;
+  const int bn = (in_group / gm) * BN;
+
+  // Copy offsets [half][j] (the instruction offset 1024 * j moves both
+  // addresses, so it is taken off the global one; rows >= 8j keep them >= 0).
+  const int crow = lane >> 3;
+  const int pch = lane & 7;
+  uint32_t a_off[2][4];
+  uint32_t b_off[2][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 32 * wave + 8 * j + crow;
+    const int lch = pch ^ ((row >> 1) & 7);
+    a_off[0][j] = static_cast<uint32_t>(row * lda + lch * 8) * 2u - 1024u * j;
+    b_off[0][j] = static_cast<uint32_t>(row * ldb + lch * 8) * 2u - 1024u * j;
+    a_off[1][j] = a_off[0][j] + static_cast<uint32_t>(128 * lda) * 2u;
+    b_off[1][j] = b_off[0][j] + static_cast<uint32_t>(128 * ldb) * 2u;
+  }
+  const char* a_tile = reinterpret_cast<const char*>(A + static_cast<size_t>(bm) * lda);
+  const char* b_tile = reinterpret_cast<const char*>(Bt + static_cast<size_t>(bn) * ldb);
+  const uint32_t wave_lds = lds_addr(smem) + static_cast<uint32_t>(wave) * 4096u;
+  const int S = K / BK;
+  // Copy j of part p (its stage clamped to the last: past the end a retired
+  // slot is refilled with the last stage, unused) into `slot`.
+  auto copy_pj = [&](int p, int slot, int j) {
+    const int ty = p & 3;
+    const int st = min(p >> 2, S - 1);
+    const char* base = (ty < 2 ? a_tile : b_tile) + st * (BK * 2);
+    const uint32_t voff = ty < 2 ? a_off[ty][j] : b_off[ty - 2][j];
+    const uint32_t m0 = wave_lds + static_cast<uint32_t>(slot * PARTB);
+    switch (j) {
+      case 0: load_lds16_sbase_off<0>(voff, base, m0); break;
+      case 1: load_lds16_sbase_off<1024>(voff, base, m0); break;
+      case 2: load_lds16_sbase_off<2048>(voff, base, m0); break;
+      default: load_lds16_sbase_off<3072>(voff, base, m0); break;
+    }
+  };
+
+  // Fragment reads: lane l reads row l % 16 of a 16-row block, 16-byte chunk
+  // 4 * kk + l / 16 of k-step kk (0, 1) of the stage.  Bases rb[kk][q] =
+  // that lane part + q * 64 KiB; slot and block go into the immediate.
+  const int lrow = lane & 15;
+  const int lq = lane >> 4;
+  typedef __attribute__((address_space(3))) const char lds_char;
+  typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+  lds_char* lbase = (lds_char*)(smem);
+  lds_char* rb[2][3];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    lds_char* o = lbase + (lrow * 128 + (((4 * kk + lq) ^ ((lrow >> 1) & 7)) << 4));
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+      rb[kk][q] = o + q * 65536;
+    }
+  }
+  const int ta = wm >> 7;        // this wave's A part type
+  const int tb = 2 + (wn >> 7);  // and Bt part type
+  // fragment f (0..7: A row blocks of 16, 8..15: Bt) of k-step kk of `slot`
+  auto frag = [&](int slot, int kk, int f) -> u32x4 {
+    const int byte = slot * PARTB + (f & 7) * 2048;
+    return *reinterpret_cast<lds_u32x4*>(rb[kk][byte >> 16] + (byte & 0xffff));
+  };
+
+  floatx4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      acc[i][j] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+  }
+
+  // Prologue: stages 0 and 1 (parts 0-7 into slots 0-7), then the first k-step
+  // of stage 0 into registers.
+#pragma unroll
+  for (int p = 0; p < 8; ++p) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      copy_pj(p, p, j);
+    }
+  }
+  wait_vmcnt<16>();                    // stage 0 has landed
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // no scalar load pending at the loop head
+  stage_barrier();
+  u32x4 r0[16];
+  u32x4 r1[16];
+#pragma unroll
+  for (int f = 0; f < 16; ++f) {
+    r0[f] = frag(f < 8 ? ta : tb, 0, f);
+  }
+
+  auto body = [&](auto phase, int s) {
+    constexpr int t = decltype(phase)::value;  // s % 5
+    constexpr int sl0 = (4 * t) % NPART;       // slot of part 4s
+    constexpr int nsl = (4 * t + 4) % NPART;   // slot of part 4s + 4
+    // first half: k-step 0 on r0; r1 <- k-step 1; copies of parts 4s+8, 4s+9
+#pragma unroll
+    for (int g = 0; g < 64; ++g) {
+      acc[g >> 3][g & 7] = mfma16x16x32<T>(r0[g >> 3], r0[8 + (g & 7)], acc[g >> 3][g & 7]);
+      __builtin_amdgcn_sched_barrier(0);
+      if ((g & 1) == 0 && g < 32) {
+        const int f = g >> 1;
+        r1[f] = frag((sl0 + (f < 8 ? ta : tb)) % NPART, 1, f);
+      }
+      if ((g & 7) == 4) {
+        const int c = g >> 3;
+        copy_pj(4 * s + 8 + (c >> 2), (sl0 + 8 + (c >> 2)) % NPART, c & 3);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    wait_vmcnt<8>();    // this wave's copies of stage s + 1 have landed
+    wait_lgkmcnt<0>();  // and its reads of stage s are done
+    stage_barrier();    // everyone's: stage s + 1 is readable, stage s retires
+    // second half: k-step 1 on r1; r0 <- k-step 0 of stage s+1; copies of
+    // parts 4s+10, 4s+11
+#pragma unroll
+    for (int g = 0; g < 64; ++g) {
+      acc[g >> 3][g & 7] = mfma16x16x32<T>(r1[g >> 3], r1[8 + (g & 7)], acc[g >> 3][g & 7]);
+      __builtin_amdgcn_sched_barrier(0);
+      if ((g & 3) == 0) {
+        const int f = g >> 2;
+        r0[f] = frag((nsl + (f < 8 ? ta : tb)) % NPART, 0, f);
+      }
+      if ((g & 7) == 4) {
+        const int c = g >> 3;
+        copy_pj(4 * s + 10 + (c >> 2), (sl0 + 10 + (c >> 2)) % NPART, c & 3);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  for (int s = 0; s < S; s += 5) {
+    body(std::integral_constant<int, 0>{}, s);
+    if (s + 1 < S) body(std::integral_constant<int, 1>{}, s + 1);
+    if (s + 2 < S) body(std::integral_constant<int, 2>{}, s + 2);
+    if (s + 3 < S) body(std::integral_constant<int, 3>{}, s + 3);
+    if (s + 4 < S) body(std::integral_constant<int, 4>{}, s + 4);
+  }
+  wait_vmcnt<0>();  // no copy may still be writing LDS when the wave ends
+
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int n = bn + wn + j * 16 + lrow;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = bm + wm + i * 16 + 4 * lq + r;
+        if (m < M && n < N) {
+          epi(m, n, acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Ring-pipelined 16-bit TN GEMM for short K (the ViT block's GEMMs, K = 768).
 //
 // With K = 768 a tile has 12 stages of BK = 64 and each stage holds only a
@@ -2013,6 +2215,9 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 //          (gemm_half_tn_w4_kernel); needs A / Bt padded to 256 rows
 //   w4d    256x256, 4 waves 2x2, two 64-deep stages, two barriers per stage
 //          (gemm_half_tn_w4d_kernel); needs A / Bt padded to 256 rows
+//   w4h    256x256, 4 waves 2x2, w4r's ring with the barrier mid-stage and a
+//          half stage of fragments in registers, 16x16x32 MFMAs
+//          (gemm_half_tn_w4h_kernel); needs A / Bt padded
 //   w4r    256x256, 4 waves 2x2, ring of ten 128-byte-row parts, one barrier
 //          per 64-deep stage (gemm_half_tn_w4r_kernel); needs A / Bt padded
 //   lds    256x256, 8 waves 2x4 (128x64 each), global -> LDS direct loads
@@ -2022,7 +2227,9 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 //   mid    128x128, 4 waves 2x2 (64x64 each)
 //   small   64x64,  4 waves 2x2 (32x32 each)
 // Default: the largest tile that still gives at least one workgroup per CU
-// (w4r from one tile per CU where the operands are padded, big8 elsewhere).
+// (w4h from one tile per CU where the operands are padded, big8 elsewhere).
+// Alternating runs on one box, 8192^3 / 4096^3 bf16 TFLOP/s: w4h 1516-1529 /
+// 1464-1467, w4r 1387-1390 / 1302-1307.
 // Measured with alternating runs on one box, 8192^3 / 4096^3 bf16 TFLOP/s:
 // w4r 1281-1299 / 1271-1280, w4d 1287-1299 / 1263-1269, w4 1281-1289 /
 // 1203-1204; w4r also takes 3.5% fewer cycles at 8192^3 in the counters
@@ -2030,7 +2237,7 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 // lds stays selectable (tune cache, CJ_HIP_GEMM_TILE).
 // CJ_HIP_GEMM_TILE=<name> overrides the choice (tuning sweeps), like the
 // reference's CJ_* tuning variables.
-enum class HalfTile { kW4, kW4D, kW4R, kLds, kBig8, kBig4, kMid, kSmall };
+enum class HalfTile { kW4, kW4D, kW4R, kW4H, kLds, kBig8, kBig4, kMid, kSmall };
 
 inline int tiles_for(int M, int N, int b) { return ((M + b - 1) / b) * ((N + b - 1) / b); }
 
@@ -2040,6 +2247,7 @@ inline HalfTile pick_half_tile(int M, int N, bool padded) {
     if (v == "w4" && padded) return HalfTile::kW4;
     if (v == "w4d" && padded) return HalfTile::kW4D;
     if (v == "w4r" && padded) return HalfTile::kW4R;
+    if (v == "w4h" && padded) return HalfTile::kW4H;
     if (v == "lds" && padded) return HalfTile::kLds;
     if (v == "big8") return HalfTile::kBig8;
     if (v == "big4") return HalfTile::kBig4;
@@ -2048,7 +2256,7 @@ inline HalfTile pick_half_tile(int M, int N, bool padded) {
   }
   constexpr int kCUs = 256;
   if (tiles_for(M, N, 256) >= kCUs) {
-    return padded ? HalfTile::kW4R : HalfTile::kBig8;
+    return padded ? HalfTile::kW4H : HalfTile::kBig8;
   }
   if (tiles_for(M, N, 128) >= kCUs) {
     return HalfTile::kMid;
@@ -2073,6 +2281,7 @@ static hipError_t launch_gemm_half_tile(HalfTile tile, LoadA load_a, const uint1
     case HalfTile::kW4:
     case HalfTile::kW4D:
     case HalfTile::kW4R:
+    case HalfTile::kW4H:
     case HalfTile::kLds:
     case HalfTile::kBig8:
       return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
@@ -2120,13 +2329,17 @@ inline bool vit_ring_bk128(long long K) {
 // Its copies use 32-bit byte offsets from a stage base and 16-byte alignment.
 inline bool ring_fits(long long rows, long long ld) { return rows * ld * 2 < (1LL << 31) && ld % 8 == 0; }
 
-// W4: 0 = gemm_half_tn_w4_kernel, 1 = gemm_half_tn_w4d_kernel, 2 = gemm_half_tn_w4r_kernel
+// W4: 0 = gemm_half_tn_w4_kernel, 1 = gemm_half_tn_w4d_kernel, 2 = gemm_half_tn_w4r_kernel,
+// 3 = gemm_half_tn_w4h_kernel
 template <typename T, int W4>
 static hipError_t launch_gemm_w4(const uint16_t* A, const uint16_t* Bt, float* C, int M, int N, int K, int lda,
                                  int ldb, int ldc, hipStream_t stream) {
   const int tiles_n = (N + 255) / 256;
   const dim3 grid(((M + 255) / 256) * tiles_n);
-  if constexpr (W4 == 2) {
+  if constexpr (W4 == 3) {
+    hipLaunchKernelGGL((gemm_half_tn_w4h_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
+                       tiles_n, EpiF32{C, ldc});
+  } else if constexpr (W4 == 2) {
     hipLaunchKernelGGL((gemm_half_tn_w4r_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
                        tiles_n, EpiF32{C, ldc});
   } else if constexpr (W4 == 1) {
@@ -2228,6 +2441,7 @@ GemmHalfVariant gemmHalfChoose(int M, int N) {
     case HalfTile::kW4: return GemmHalfVariant::kW4;
     case HalfTile::kW4D: return GemmHalfVariant::kW4D;
     case HalfTile::kW4R: return GemmHalfVariant::kW4R;
+    case HalfTile::kW4H: return GemmHalfVariant::kW4H;
     case HalfTile::kLds: return GemmHalfVariant::kLds;
     case HalfTile::kBig8: return GemmHalfVariant::kBig8;
     case HalfTile::kBig4: return GemmHalfVariant::kBig4;
@@ -2267,7 +2481,7 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
   // A and Bt come from the resident upload, padded to 256 rows; the copies'
   // 32-bit lane offsets reach 256 rows of either operand.
   if ((variant == GemmHalfVariant::kLds || variant == GemmHalfVariant::kW4 || variant == GemmHalfVariant::kW4D ||
-       variant == GemmHalfVariant::kW4R) &&
+       variant == GemmHalfVariant::kW4R || variant == GemmHalfVariant::kW4H) &&
       (256LL * lda * 2 >= (1LL << 31) || 256LL * ldb * 2 >= (1LL << 31))) {
     variant = GemmHalfVariant::kBig8;
   }
@@ -2278,6 +2492,10 @@ hipError_t gemmHalfTN(const uint16_t* A, const uint16_t* Bt, float* C, int M, in
   if (variant == GemmHalfVariant::kW4D && K > 0) {
     return t == Half::kBF16 ? launch_gemm_w4<BF16, 1>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
                             : launch_gemm_w4<F16, 1>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
+  }
+  if (variant == GemmHalfVariant::kW4H && K > 0) {
+    return t == Half::kBF16 ? launch_gemm_w4<BF16, 3>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)
+                            : launch_gemm_w4<F16, 3>(A, Bt, C, M, N, K, lda, ldb, ldc, stream);
   }
   if (variant == GemmHalfVariant::kW4R && K > 0) {
     return t == Half::kBF16 ? launch_gemm_w4<BF16, 2>(A, Bt, C, M, N, K, lda, ldb, ldc, stream)

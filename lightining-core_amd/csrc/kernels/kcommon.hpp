@@ -5,6 +5,8 @@
 //   v_mfma_f32_32x32x16_bf16 A: A[m = l%32][k = 8(l/32)+j] B: B[k = 8(l/32)+j][n = l%32], j = 0..7
 //   (f16 the same)
 //   32x32 accumulator (16 regs): D[m = 8(i/4) + 4(l/32) + i%4][n = l%32], i = 0..15
+//   v_mfma_f32_16x16x32_bf16 A: A[m = l%16][k = 8(l/16)+j] B: B[k = 8(l/16)+j][n = l%16], j = 0..7
+//   16x16 accumulator (4 regs):   D[m = 4(l/16) + i][n = l%16], i = 0..3
 // Any permutation of k applied identically to A and B leaves the product
 // unchanged; the attention kernels use that to feed softmax probabilities to
 // the second MFMA straight from the first MFMA's accumulator registers.
@@ -109,6 +111,20 @@ __device__ __forceinline__ floatx16 mfma32x32x16<F16>(u32x4 a, u32x4 b, floatx16
                                                 0);
 }
 
+// 16x16x32 MFMA on 8 packed 16-bit values per lane (as four dwords).
+template <typename T>
+__device__ __forceinline__ floatx4 mfma16x16x32(u32x4 a, u32x4 b, floatx4 c);
+template <>
+__device__ __forceinline__ floatx4 mfma16x16x32<BF16>(u32x4 a, u32x4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                 0, 0);
+}
+template <>
+__device__ __forceinline__ floatx4 mfma16x16x32<F16>(u32x4 a, u32x4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                0);
+}
+
 __device__ __forceinline__ floatx16 mfma32x32x2f32(float a, float b, floatx16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
@@ -153,6 +169,21 @@ __device__ __forceinline__ void load_lds16_sbase(uint32_t voff, const void* sbas
                : "memory");
 }
 
+// The same copy with an instruction offset OFF (0..4095 bytes), which the
+// hardware adds to both the global and the LDS address (measured on gfx950:
+// lane l's 16 bytes from sbase + voff + OFF land at lds + OFF + 16*l).  Copies
+// that fill consecutive 1 KB blocks of LDS can then share one M0 value, with
+// OFF = 1024 * j and voff reduced by the same OFF.
+template <int OFF>
+__device__ __forceinline__ void load_lds16_sbase_off(uint32_t voff, const void* sbase, uint32_t lds) {
+  static_assert(OFF >= 0 && OFF < 4096, "instruction offset");
+  uint64_t base;
+  asm volatile("s_mov_b64 %0, %2\n\tglobal_load_lds_dwordx4 %1, %0 offset:%3"
+               : "=&s"(base)
+               : "v"(voff), "s"(sbase), "i"(OFF), "{m0}"(lds)
+               : "memory");
+}
+
 // LDS byte address of a __shared__ object, as a wave-uniform value.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));
@@ -164,6 +195,13 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt immediate");
   __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
+// s_waitcnt lgkmcnt(n) (vmcnt / expcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt immediate");
+  __builtin_amdgcn_s_waitcnt((0xc07f & ~(0xf << 8)) | (N << 8));
 }
 
 // Workgroup barrier without the release fence of __syncthreads(): the fence

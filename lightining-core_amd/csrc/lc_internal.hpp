@@ -138,6 +138,10 @@ struct HipContext {
   // Split-K workspace of the skinny 16-bit GEMM (partials + per-column-tile
   // counters, zero at allocation and after every launch); `stream` only.
   DeviceBuffer skinny_part, skinny_counters;
+  // Enqueue-only launches since the stream was last synchronised, per op
+  // family (noteEnqueued; syncStream resets both).
+  std::size_t matmul_inflight = 0;
+  std::size_t attention_inflight = 0;
 };
 
 bool hipAvailable();
@@ -151,6 +155,16 @@ Status download(HipContext* ctx, void* dst, const void* src, std::size_t bytes);
 // Synchronises the backend stream, then reports a failure a kernel recorded
 // since the last sync (a stream-K wait that ran out) as kDriverError.
 Status syncStream(HipContext* ctx);
+// Bookkeeping of enqueue-only launches (no download, no synchronize), as the
+// reference's backends cap their in-flight submissions: matmul at 256
+// (src/ops/matmul_metal.mm:27, :1864-1878, :1969-1973, :2066-2070),
+// attention at 64 (src/attention_metal.mm:26, :1448-1462, :2149-2157).
+// Adds `launches` to the op family's count; at the cap the stream is
+// synchronised (a device_synchronize trace event with size_bytes = the count,
+// detail0 = the op, detail1 = 1) and the count restarts.
+constexpr std::size_t kMatMulMaxInflight = 256;
+constexpr std::size_t kAttentionMaxInflight = 64;
+Status noteEnqueued(HipContext* ctx, TraceOp op, std::size_t launches);
 // The epoch for the next stream-K launch over gemm_flags (clears the flags
 // on the stream when the counter wraps).
 Status nextStreamKEpoch(HipContext* ctx, int* epoch);

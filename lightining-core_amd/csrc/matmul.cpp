@@ -14,6 +14,7 @@
 // 16-bit compute rounds the fp32 host data once at upload (RNE) and lays B out
 // K-contiguous (transposed), the layout the MFMA GEMM reads.
 #include <algorithm>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <iterator>
@@ -82,24 +83,33 @@ struct VariantInfo {
   int variant;
   const char* name;
   int tile_m, tile_n, tile_k, waves, split_k;
+  const char* hip_kernel;  // the __global__ function that runs it
 };
 
 constexpr VariantInfo kF32Variants[] = {
-    {static_cast<int>(kern::GemmF32Variant::kDataParallel), "f32_dp_64x64x64", 64, 64, 64, 8, 2},
-    {static_cast<int>(kern::GemmF32Variant::kStreamK), "f32_streamk_64x64x64", 64, 64, 64, 8, 2},
-    {static_cast<int>(kern::GemmF32Variant::kDataParallelBK32), "f32_dp_64x64x32", 64, 64, 32, 8, 2},
+    {static_cast<int>(kern::GemmF32Variant::kDataParallel), "f32_dp_64x64x64", 64, 64, 64, 8, 2,
+     "gemm_f32_lds_kernel"},
+    {static_cast<int>(kern::GemmF32Variant::kStreamK), "f32_streamk_64x64x64", 64, 64, 64, 8, 2,
+     "gemm_f32_lds_kernel"},
+    {static_cast<int>(kern::GemmF32Variant::kDataParallelBK32), "f32_dp_64x64x32", 64, 64, 32, 8, 2,
+     "gemm_f32_lds_kernel"},
 };
 
 constexpr VariantInfo kHalfVariants[] = {
-    {static_cast<int>(kern::GemmHalfVariant::kW4), "half_w4_256x256", 256, 256, 32, 4, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kW4D), "half_w4d_256x256", 256, 256, 64, 4, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kW4R), "half_w4r_256x256", 256, 256, 64, 4, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kLds), "half_lds_256x256", 256, 256, 64, 8, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kBig8), "half_big8_256x256", 256, 256, 64, 8, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kBig4), "half_big4_256x256", 256, 256, 64, 4, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kMid), "half_mid_128x128", 128, 128, 64, 4, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kSmall), "half_small_64x64", 64, 64, 64, 4, 1},
-    {static_cast<int>(kern::GemmHalfVariant::kSkinny), "half_skinny_16x64", 16, 64, 256, 8, 2},
+    {static_cast<int>(kern::GemmHalfVariant::kW4), "half_w4_256x256", 256, 256, 32, 4, 1, "gemm_half_tn_w4_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kW4D), "half_w4d_256x256", 256, 256, 64, 4, 1,
+     "gemm_half_tn_w4d_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kW4R), "half_w4r_256x256", 256, 256, 64, 4, 1,
+     "gemm_half_tn_w4r_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kW4H), "half_w4h_256x256", 256, 256, 64, 4, 1,
+     "gemm_half_tn_w4h_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kLds), "half_lds_256x256", 256, 256, 64, 8, 1,
+     "gemm_half_tn_lds_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kBig8), "half_big8_256x256", 256, 256, 64, 8, 1, "gemm_half_tn_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kBig4), "half_big4_256x256", 256, 256, 64, 4, 1, "gemm_half_tn_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kMid), "half_mid_128x128", 128, 128, 64, 4, 1, "gemm_half_tn_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kSmall), "half_small_64x64", 64, 64, 64, 4, 1, "gemm_half_tn_kernel"},
+    {static_cast<int>(kern::GemmHalfVariant::kSkinny), "half_skinny_16x64", 16, 64, 256, 8, 2, "gemm_skinny_kernel"},
 };
 
 struct VariantTable {
@@ -338,6 +348,8 @@ Status matmulResident(HipContext* ctx, MatMulResident& r, std::size_t m, std::si
   }
   if (policy.download_out || policy.synchronize) {
     LC_TRY(syncStream(ctx));
+  } else if (repeat > 0) {
+    LC_TRY(noteEnqueued(ctx, TraceOp::kMatMul, repeat));
   }
   return Status::kSuccess;
 }
@@ -497,6 +509,91 @@ lcError_t lcMatMulResidentSessionRunBatchSyncNoDownload(lcMatMulResidentSession*
 // ops.hpp:1371-1373: the same with null pointers.
 lcError_t lcMatMulResidentSessionRunBatchSyncCachedNoDownload(lcMatMulResidentSession* s, size_t repeat_count) {
   return lcMatMulResidentSessionRunBatchSyncNoDownload(s, nullptr, nullptr, nullptr, repeat_count);
+}
+
+lcError_t lcMatMulResidentSessionTimeLaunches(lcMatMulResidentSession* s, size_t count, float* ms_out) {
+  if (s == nullptr || count == 0 || ms_out == nullptr) {
+    return toLc(fail(Status::kInvalidValue, "matmul session: null session or output, or count 0"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(LC_DEVICE_HIP, "matmul session", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  MatMulResident& r = s->res;
+  if (!r.has_a || !r.has_b || r.m != s->m || r.k != s->k || r.n != s->n || r.dtype != s->dtype) {
+    return toLc(fail(Status::kInvalidValue, "matmul session: no resident inputs to time (start the session first)"));
+  }
+  if (!r.tuned) {
+    st = settleVariant(ctx, r);
+    if (st != Status::kSuccess) {
+      return toLc(st);
+    }
+    r.tuned = true;
+  }
+  std::vector<hipEvent_t> ev(2 * count, nullptr);
+  hipError_t e = hipSuccess;
+  for (std::size_t i = 0; i < ev.size() && e == hipSuccess; ++i) {
+    e = hipEventCreate(&ev[i]);
+  }
+  for (std::size_t i = 0; i < count && e == hipSuccess; ++i) {
+    e = hipEventRecord(ev[2 * i], ctx->stream);
+    if (e == hipSuccess) {
+      traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, r.m * r.k * r.n);
+      e = launchGemm(ctx, r, r.variant);
+    }
+    if (e == hipSuccess) {
+      e = hipEventRecord(ev[2 * i + 1], ctx->stream);
+    }
+  }
+  if (e == hipSuccess) {
+    e = hipStreamSynchronize(ctx->stream);
+  }
+  for (std::size_t i = 0; i < count && e == hipSuccess; ++i) {
+    e = hipEventElapsedTime(&ms_out[i], ev[2 * i], ev[2 * i + 1]);
+  }
+  for (hipEvent_t x : ev) {
+    if (x != nullptr) {
+      (void)hipEventDestroy(x);
+    }
+  }
+  if (e != hipSuccess) {
+    return toLc(failHip(e, "matmul session: timed launches"));
+  }
+  r.has_c = true;
+  return toLc(syncStream(ctx));
+}
+
+lcError_t lcMatMulResidentSessionKernelName(lcMatMulResidentSession* s, char* buf, size_t cap) {
+  if (s == nullptr || buf == nullptr || cap == 0) {
+    return toLc(fail(Status::kInvalidValue, "matmul session: null session or buffer"));
+  }
+  HipContext* ctx = nullptr;
+  Status st = requireHip(LC_DEVICE_HIP, "matmul session", &ctx);
+  if (st != Status::kSuccess) {
+    return toLc(st);
+  }
+  std::lock_guard<std::recursive_mutex> lock(ctx->mu);
+  const bool half = isHalf(s->dtype);
+  int v = s->res.tuned ? s->res.variant : 0;
+  if (v == 0) {
+    const int groups = ctx->props.multiProcessorCount > 0 ? ctx->props.multiProcessorCount : 256;
+    v = half ? (s->m <= 16 ? static_cast<int>(kern::GemmHalfVariant::kSkinny)
+                           : static_cast<int>(kern::gemmHalfChoose(static_cast<int>(s->m), static_cast<int>(s->n))))
+             : static_cast<int>(kern::gemmF32Choose(static_cast<int>(s->m), static_cast<int>(s->n), groups));
+  }
+  std::string text;
+  for (const VariantInfo& info : variants(half)) {
+    if (info.variant == v) {
+      text = std::string(info.name) + " " + info.hip_kernel;
+    }
+  }
+  if (text.empty()) {
+    return toLc(fail(Status::kUnknown, "matmul session: unknown variant"));
+  }
+  std::snprintf(buf, cap, "%s", text.c_str());
+  return LC_SUCCESS;
 }
 
 }  // extern "C"

@@ -2,11 +2,14 @@
 //
 // lcMatMulDeviceNoAlloc computes C = A . B like lcMatMul, with the same
 // kernels (gemm_f32_lds_kernel, whole tiles or stream-K), for callers that
-// cannot allocate device memory: code under HIP graph capture, tight serving
-// loops, harnesses that forbid hipMalloc.  The caller passes device-resident
-// A, B and C; every other byte the kernels touch lives in `scratch`, a
-// file-scope device array of kScratchBytes that each GPU holds until the
-// process ends:
+// cannot allocate device memory: tight serving loops and harnesses that
+// forbid hipMalloc.  It is a synchronous call on the library's own stream:
+// it clears the failure word (hipMemsetAsync), launches, copies the failure
+// word to the host and synchronises that stream before returning, so it must
+// not be called while a stream capture is active (it records nothing into a
+// caller's graph).  The caller passes device-resident A, B and C; every other
+// byte the kernels touch lives in `scratch`, a file-scope device array of
+// kScratchBytes that each GPU holds until the process ends:
 //
 //   [0, 4 MiB)          stream-K partial tiles (256 workgroups x 64 x 64 fp32)
 //   [4 MiB, +1 KiB)     stream-K ready flags (256 ints)
@@ -20,10 +23,11 @@
 // current) and kept per device.  All calls on one GPU share that GPU's array,
 // which keeps the last call's contents: the kernel clears the flags it
 // consumed and each launch publishes with a new epoch (so a flag a timed-out
-// launch left set is never taken for ready); the failure word is cleared on
-// the stream before each launch.  Calls hold the library's context mutex, so
-// calls from threads of one process are serialised; calls that overlap on
-// one GPU from different processes or outside the library race.
+// launch left set is never taken for ready), and after a launch whose wait
+// ran out the flags are zeroed before the call returns; the failure word is
+// cleared on the stream before each launch.  Calls hold the library's context
+// mutex, so calls from threads of one process are serialised; calls that
+// overlap on one GPU from different processes or outside the library race.
 #include <algorithm>
 #include <cstddef>
 #include <cstdint>
@@ -155,6 +159,10 @@ Status matmulDeviceNoAlloc(const float* a, const float* b, float* c, std::size_t
   LC_HIP_TRY(hipMemcpyAsync(&failed, fail_word, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
   LC_TRY(syncStream(ctx));
   if (failed != 0) {
+    // The kernel has completed, so no publisher is still running: zero the
+    // flags a late publisher may have set, so no later launch can meet them.
+    LC_HIP_TRY(hipMemsetAsync(base + kFlagsOffset, 0, kMaxGroups * sizeof(int), ctx->stream));
+    LC_HIP_TRY(hipStreamSynchronize(ctx->stream));
     return fail(Status::kDriverError,
                 "matmul no-alloc: a stream-K workgroup's bounded wait for a partial tile ran out "
                 "(CJ_HIP_STREAMK_SPIN_LIMIT); the result is invalid");

@@ -40,6 +40,10 @@ Status fail(Status st, const std::string& msg) {
 }
 
 Status failHip(hipError_t e, const char* what) {
+  // The error is reported here; clear HIP's per-thread last error so the next
+  // launch's hipGetLastError() does not report it again (a failed hipMalloc
+  // would otherwise fail the next kernel launch).
+  (void)hipGetLastError();
   Status st = Status::kDriverError;
   if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
     st = Status::kOutOfMemory;
@@ -254,14 +258,37 @@ Status download(HipContext* ctx, void* dst, const void* src, std::size_t bytes) 
 
 Status syncStream(HipContext* ctx) {
   LC_HIP_TRY(hipStreamSynchronize(ctx->stream));
+  ctx->matmul_inflight = 0;
+  ctx->attention_inflight = 0;
   if (int* word = static_cast<int*>(ctx->gemm_fail.get())) {
     if (__atomic_exchange_n(word, 0, __ATOMIC_ACQ_REL) != 0) {
+      // The stream is idle, so the launch whose wait ran out has completed:
+      // zero the flags a late publisher may have set with that launch's
+      // epoch, so a replay of a captured launch (which reuses its epoch)
+      // cannot take them for ready.
+      if (void* flags = ctx->gemm_flags.get()) {
+        LC_HIP_TRY(hipMemsetAsync(flags, 0, ctx->gemm_flags.size(), ctx->stream));
+        LC_HIP_TRY(hipStreamSynchronize(ctx->stream));
+      }
       return fail(Status::kDriverError,
                   "matmul: a stream-K workgroup's bounded wait for a partial tile ran out "
                   "(CJ_HIP_STREAMK_SPIN_LIMIT); the result of that launch is invalid");
     }
   }
   return Status::kSuccess;
+}
+
+Status noteEnqueued(HipContext* ctx, TraceOp op, std::size_t launches) {
+  const bool mm = op == TraceOp::kMatMul;
+  std::size_t& count = mm ? ctx->matmul_inflight : ctx->attention_inflight;
+  count += launches;
+  if (count < (mm ? kMatMulMaxInflight : kAttentionMaxInflight)) {
+    return Status::kSuccess;
+  }
+  const std::size_t was = count;
+  const Status st = syncStream(ctx);
+  traceRecord(TraceEventType::kDeviceSynchronize, st, was, static_cast<int>(op), 1);
+  return st;
 }
 
 Status nextStreamKEpoch(HipContext* ctx, int* epoch) {

@@ -604,6 +604,20 @@ class MatMulResidentSession:
     def run_batch_sync_cached_no_download(self, repeat_count: int):
         _check(_lib().lcMatMulResidentSessionRunBatchSyncCachedNoDownload(self._h, repeat_count))
 
+    def time_launches(self, count: int) -> np.ndarray:
+        """Per-launch durations (ms) of `count` launch-only GEMMs on the resident
+        inputs, a hipEvent pair around each (measurement helper; no reference
+        counterpart)."""
+        ms = np.zeros(count, np.float32)
+        _check(_lib().lcMatMulResidentSessionTimeLaunches(self._h, count, ms.ctypes.data_as(ctypes.c_void_p)))
+        return ms
+
+    def kernel_name(self) -> str:
+        """"<tune-cache variant> <kernel function>" of the GEMM this shape runs."""
+        buf = ctypes.create_string_buffer(128)
+        _check(_lib().lcMatMulResidentSessionKernelName(self._h, buf, len(buf)))
+        return buf.value.decode()
+
     # reference list-returning names (bind_ops.cpp:196-240)
     def start(self, a, b, out_size=None):
         return self.start_into(a, b)

@@ -198,6 +198,8 @@ SIGNATURES = {
     "lcMatMulResidentSessionRunBatchSync": (_E, [c_void_p, BUF, BUF, BUF, c_size]),
     "lcMatMulResidentSessionRunBatchSyncNoDownload": (_E, [c_void_p, BUF, BUF, BUF, c_size]),
     "lcMatMulResidentSessionRunBatchSyncCachedNoDownload": (_E, [c_void_p, c_size]),
+    "lcMatMulResidentSessionTimeLaunches": (_E, [c_void_p, c_size, c_void_p]),
+    "lcMatMulResidentSessionKernelName": (_E, [c_void_p, ctypes.c_char_p, c_size]),
     "lcConv2dNchw": (_E, [BUF, BUF, BUF, BUF] + [c_size] * 11 + [c_int, c_int]),
     "lcConvAttentionTorchstrongNchw": (_E, [BUF, BUF, BUF, BUF] + [c_size] * 13 + [c_int]),
     "lcConvAttentionTorchstrongNchwGraph": (_E, [BUF, BUF, BUF, BUF] + [c_size] * 13 + [c_int]),

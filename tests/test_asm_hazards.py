@@ -12,8 +12,14 @@ apply to these copies (AMD CDNA3/CDNA4 ISA, "manually inserted wait states"):
 * an SALU write of M0 needs 1 wait state before an LDS-DMA load reads M0
   (the SALU copy above is that wait state); a VALU write of M0 would need 5.
 
-The scan checks every LDS-DMA load in the compiled kernels for both, and a
-planted instance of the faulting sequence shows the scan catches it.
+A third check covers a second fault of the same family, in host-visible
+kernel code rather than the asm: a 64-bit base rebuilt from a 32-bit
+v_readfirstlane result, whose high half then came from sign-extending the low
+half (s_ashr_i32 hi, lo, 31) instead of from the pointer.  The scan traces
+each copy's base pair back to its last writers and flags that shape.
+
+The scan checks every LDS-DMA load in the compiled kernels, and planted
+instances of the faulting sequences show the scan catches them.
 """
 import concurrent.futures
 import glob
@@ -52,9 +58,43 @@ def _instructions(text):
     return out
 
 
+def _dest(t):
+    """SGPRs an instruction writes (its first operand), for s_* and v_* ops."""
+    parts = t.split(None, 1)
+    if len(parts) < 2 or not (parts[0].startswith("s_") or parts[0].startswith("v_")):
+        return set()
+    return _sregs(parts[1].split(",")[0])
+
+
+def _last_writer(ins, i, reg):
+    """Index of the last instruction before i that writes `reg` (None at a
+    label: a control-flow merge ends the straight-line trace)."""
+    for j in range(i - 1, -1, -1):
+        if ins[j].endswith(":"):
+            return None
+        if reg in _dest(ins[j]):
+            return j
+    return None
+
+
+def _sign_extended_readfirstlane_base(ins, i, pair):
+    """The copy at i reads `pair`: is its high half s_ashr_i32 of its low
+    half, with the low half written by v_readfirstlane?"""
+    m = re.match(r"s\[(\d+):(\d+)\]$", pair)
+    if not m:
+        return False
+    lo, hi = f"s{m.group(1)}", f"s{m.group(2)}"
+    j = _last_writer(ins, i, hi)
+    if j is None or not re.match(rf"^s_ashr_i32\s+{hi},\s*{lo},\s*31$", ins[j]):
+        return False
+    k = _last_writer(ins, j, lo)
+    return k is not None and ins[k].startswith("v_readfirstlane_b32")
+
+
 def scan(text):
     """Problems found: LDS-DMA loads whose SGPR base is not an SALU copy made
-    by the instruction right before, and VALU writes of M0."""
+    by the instruction right before, bases whose high half is a sign-extended
+    v_readfirstlane result, and VALU writes of M0."""
     problems = []
     ins = _instructions(text)
     for i, t in enumerate(ins):
@@ -65,9 +105,14 @@ def scan(text):
             continue
         base = m.group(1)
         prev = ins[i - 1] if i > 0 else ""
-        pm = re.match(r"^s_mov_b64\s+(s\[\d+:\d+\]),", prev)
+        pm = re.match(r"^s_mov_b64\s+(s\[\d+:\d+\]),\s*(s\[\d+:\d+\])$", prev)
         if not pm or pm.group(1) != base:
             problems.append(f"load reads {base} not copied by the previous SALU move: [{prev}] -> [{t}]")
+            src = base
+        else:
+            src = pm.group(2)
+        if _sign_extended_readfirstlane_base(ins, i - 1 if pm else i, src):
+            problems.append(f"load base {src} is a sign-extended v_readfirstlane value: [{t}]")
     return problems
 
 
@@ -95,6 +140,33 @@ def test_scan_catches_the_faulting_sequence():
     fixed = planted.replace("s_nop 0", "s_mov_b64 s[40:41], s[6:7]").replace("v195, s[6:7]", "v195, s[40:41]")
     assert scan(fixed) == []
     assert scan("\tv_readfirstlane_b32 m0, v3\n") != []
+
+
+def test_scan_catches_a_sign_extended_readfirstlane_base():
+    planted = "\n".join([
+        "\tv_readfirstlane_b32 s10, v5",
+        "\ts_ashr_i32 s11, s10, 31",
+        "\ts_mov_b32 m0, s3",
+        "\t;;#ASMSTART",
+        "\ts_mov_b64 s[40:41], s[10:11]",
+        "\tglobal_load_lds_dwordx4 v1, s[40:41] offset:1024",
+        "\t;;#ASMEND",
+    ])
+    found = scan(planted)
+    assert len(found) == 1 and "sign-extended" in found[0], found
+    # a base built by 64-bit adds from the kernel argument is fine, and so is
+    # a sign-extended 32-bit offset that is added to the base
+    fixed = "\n".join([
+        "\tv_readfirstlane_b32 s10, v5",
+        "\ts_ashr_i32 s11, s10, 31",
+        "\ts_lshl_b64 s[10:11], s[10:11], 1",
+        "\ts_add_u32 s12, s4, s10",
+        "\ts_addc_u32 s13, s5, s11",
+        "\ts_mov_b32 m0, s3",
+        "\ts_mov_b64 s[40:41], s[12:13]",
+        "\tglobal_load_lds_dwordx4 v1, s[40:41]",
+    ])
+    assert scan(fixed) == []
 
 
 @pytest.mark.skipif(not shutil.which(HIPCC) and not os.path.exists(HIPCC), reason="hipcc not available")

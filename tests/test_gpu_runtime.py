@@ -10,7 +10,14 @@
   session used from 4 threads, both checked against the CPU oracle;
 * the stream-K GEMM's bounded wait: with the spin limit forced to 0 from the
   host every owner gives up at once (every kernel still exits), the call
-  reports LC_DRIVER_ERROR, and the next GEMM is correct.
+  reports LC_DRIVER_ERROR, and the next GEMM is correct;
+* an allocation no device can hold reports LC_OUT_OF_MEMORY
+  (src/runtime.cpp:193-214, the kOutOfMemory status);
+* the in-flight cap of enqueue-only launches (matmul 256,
+  src/ops/matmul_metal.mm:27, :1864-1878; attention 64,
+  src/attention_metal.mm:26, :1448-1462): the capped call synchronises the
+  stream and records a device_synchronize trace event, and the results of
+  the enqueued launches match the oracle.
 """
 import ctypes
 import os
@@ -188,3 +195,73 @@ def test_streamk_wait_timeout_is_reported(lc, oracle):
                 os.environ.pop(key, None)
             else:
                 os.environ[key] = val
+
+
+def test_oversize_malloc_reports_out_of_memory(lc):
+    lib = N.load()
+    p = ctypes.c_void_p()
+    note("[case] lcMalloc of 1 PiB")
+    assert lib.lcMalloc(ctypes.byref(p), 1 << 50) == N.LC_OUT_OF_MEMORY
+    assert not p.value
+    assert "hipMalloc" in lib.lcGetLastErrorMessage().decode()
+    # the failure is not sticky: the next allocation and a sync succeed
+    assert lib.lcMalloc(ctypes.byref(p), 4096) == N.LC_SUCCESS
+    assert lib.lcFree(p) == N.LC_SUCCESS
+    assert lib.lcDeviceSynchronize() == N.LC_SUCCESS
+
+
+def _forced_syncs(op_code):
+    return [e for e in lc_trace() if e["type"] == "device_synchronize" and e["detail1"] == 1
+            and e["detail0"] == op_code]
+
+
+def lc_trace():
+    import lightning_core
+    return lightning_core.runtime_trace_events()
+
+
+def test_enqueue_only_launches_are_capped(lc, oracle):
+    m, k, n = 96, 64, 80
+    a, b = synth.uniform((m, k), stream=41), synth.uniform((k, n), stream=42)
+    ref = oracle.matmul(a, b)
+    lc.runtime_trace_enable(True)
+    try:
+        # upload once and synchronise, then 300 launch-only calls: the 256th
+        # reaches the cap and synchronises; then a downloading call
+        lc.matmul_with_policy(a, b, m, k, n, policy=lc.MatMulIoPolicy(True, True, False, True))
+        lc.runtime_trace_clear()
+        launch_only = lc.MatMulIoPolicy(False, False, False, False)
+        note("[case] 300 enqueue-only matmul calls")
+        for _ in range(300):
+            lc.matmul_with_policy(None, None, m, k, n, policy=launch_only)
+        forced = _forced_syncs(1)
+        assert len(forced) == 1, forced
+        assert forced[0]["size_bytes"] == 256 and forced[0]["status"] == lc_status_name(N.LC_SUCCESS)
+        out = lc.matmul_with_policy(None, None, m, k, n, policy=lc.MatMulIoPolicy(False, False, True, True))
+        assert_parity(ref, out.reshape(m, n), "f32", "matmul after 300 enqueue-only launches")
+        # attention sessions: 100 launch-only forwards, the 64th synchronises
+        s, d = 64, 32
+        q, kk, v = (synth.normal((s, d), stream=43 + i) for i in range(3))
+        sess = lc.AttentionSession(s, d, causal=True)
+        sess.forward_with_policy(q, kk, v, lc.AttentionIoPolicy(download_out=False, synchronize=True))
+        lc.runtime_trace_clear()
+        pol = lc.AttentionIoPolicy(upload_q=False, upload_k=False, upload_v=False, download_out=False,
+                                   synchronize=False)
+        note("[case] 100 enqueue-only attention forwards")
+        for _ in range(100):
+            sess.forward_with_policy(q, kk, v, pol)
+        forced = _forced_syncs(6)
+        assert len(forced) == 1, forced
+        assert forced[0]["size_bytes"] == 64
+        got = sess.forward_with_policy(q, kk, v, lc.AttentionIoPolicy(upload_q=False, upload_k=False,
+                                                                      upload_v=False))
+        assert_parity(oracle.attention(q, kk, v, True), got.reshape(s, d), "f32",
+                      "attention after 100 enqueue-only launches")
+        sess.close()
+    finally:
+        lc.runtime_trace_enable(False)
+        lc.runtime_trace_clear()
+
+
+def lc_status_name(code):
+    return N.load().lcGetErrorString(code).decode()

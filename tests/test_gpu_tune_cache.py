@@ -90,12 +90,15 @@ HALF_CASES = [("half_w4_256x256", (300, 129, 200)), ("half_w4_256x256", (520, 25
               ("half_w4d_256x256", (300, 129, 200)), ("half_w4d_256x256", (520, 64, 130)),
               ("half_w4r_256x256", (300, 129, 200)), ("half_w4r_256x256", (520, 64, 130)),
               ("half_w4r_256x256", (700, 1000, 513)),
+              ("half_w4h_256x256", (300, 129, 200)), ("half_w4h_256x256", (520, 64, 130)),
+              ("half_w4h_256x256", (700, 1000, 513)), ("half_w4h_256x256", (256, 1728, 512)),
               ("half_lds_256x256", (300, 129, 200)), ("half_big8_256x256", (300, 129, 200)),
               ("half_big4_256x256", (520, 256, 130)), ("half_mid_128x128", (77, 320, 513)),
               ("half_small_64x64", (1000, 777, 1030)), ("half_skinny_16x64", (9, 200, 300))]
 _TILES = {"f32_dp_64x64x64": "64,64,64,8,2", "f32_streamk_64x64x64": "64,64,64,8,2",
           "f32_dp_64x64x32": "64,64,32,8,2", "half_w4_256x256": "256,256,32,4,1",
           "half_w4d_256x256": "256,256,64,4,1", "half_w4r_256x256": "256,256,64,4,1",
+          "half_w4h_256x256": "256,256,64,4,1",
           "half_lds_256x256": "256,256,64,8,1",
           "half_big8_256x256": "256,256,64,8,1", "half_big4_256x256": "256,256,64,4,1",
           "half_mid_128x128": "128,128,64,4,1", "half_small_64x64": "64,64,64,4,1",
@@ -144,15 +147,18 @@ def test_forced_gemm_variants(lc, tmp_path, dtype, cases):
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 def test_w4_gemm_matches_lds_bitwise(lc, tmp_path, dtype):
     # The 4-wave kernels (ring of 32-deep slices; two 64-deep stages; ring
-    # of 128-byte-row parts) accumulate every output in the same k order as
-    # the 8-wave kernel: forced one after the other on the same inputs, the
-    # four must agree bit for bit (ragged M / N / K, one and many k stages,
-    # more stages than ring slots).
+    # of 128-byte-row parts, with the barrier at the end or in the middle of
+    # a stage) accumulate every output in the same k order as the 8-wave
+    # kernel: forced one after the other on the same inputs, the five must
+    # agree bit for bit (ragged M / N / K, one and many k stages, more stages
+    # than ring slots, stage counts that are and are not multiples of w4h's
+    # five-stage unroll).
     code = {"bf16": 1, "f16": 2}[dtype]
     shapes = [(600, 320, 700), (1100, 1024, 1300), (257, 64, 255), (300, 1728, 260)]
     jobs = []
     for m, k, n in shapes:
-        for name in ("half_lds_256x256", "half_w4_256x256", "half_w4d_256x256", "half_w4r_256x256"):
+        for name in ("half_lds_256x256", "half_w4_256x256", "half_w4d_256x256", "half_w4r_256x256",
+                     "half_w4h_256x256"):
             cache = tmp_path / f"mm_{name}_{m}_{k}_{n}.csv"
             cache.write_text("#lc_tune_cache,matmul,2\n" + f"{m},{k},{n},{code},gfx950,{name},{_TILES[name]}\n")
             jobs.append((str(cache), name, m, k, n))
@@ -181,10 +187,12 @@ def test_w4_gemm_matches_lds_bitwise(lc, tmp_path, dtype):
             sums.setdefault((m, k, n), {})[name] = digest
     assert len(sums) == len(shapes)
     for shape, by_name in sums.items():
-        note(f"[parity] w4 / w4d vs lds {dtype} {shape}: {'identical' if len(set(by_name.values())) == 1 else 'DIFFER'}")
+        note(f"[parity] w4 / w4d / w4r / w4h vs lds {dtype} {shape}: "
+             f"{'identical' if len(set(by_name.values())) == 1 else 'DIFFER'}")
         assert by_name["half_w4_256x256"] == by_name["half_lds_256x256"], shape
         assert by_name["half_w4r_256x256"] == by_name["half_lds_256x256"], shape
         assert by_name["half_w4d_256x256"] == by_name["half_lds_256x256"], shape
+        assert by_name["half_w4h_256x256"] == by_name["half_lds_256x256"], shape
 
 
 @pytest.mark.parametrize("s,d,causal", [(256, 64, False), (200, 48, True), (130, 96, False), (256, 64, True),

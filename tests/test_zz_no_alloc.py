@@ -7,7 +7,10 @@ first call's contents: stale partial tiles, flags of an earlier epoch); each
 result is checked against lcMatMul's on the same inputs and against the
 oracle, to the fp32 bar (normwise 1e-4).  Shapes cover whole tiles, stream-K
 split tiles, padded operands (dims not multiples of 64) and a misaligned
-base; a shape whose padded copies exceed the scratch is refused.
+base; a shape whose padded copies exceed the scratch is refused.  The
+defining property is checked directly too: after one warm-up call (module
+load, the symbol's address), free device memory as HIP reports it does not
+move across calls that pad, misalign and split tiles with stream-K.
 """
 import ctypes
 
@@ -114,5 +117,53 @@ def test_no_alloc_refuses_what_it_cannot_hold(lc):
         assert lib.lcMatMulDeviceNoAlloc(None, ctypes.c_void_p(d), ctypes.c_void_p(d), 8, 8, 8) == N.LC_INVALID_VALUE
         assert lib.lcMatMulDeviceNoAlloc(ctypes.c_void_p(d), ctypes.c_void_p(d), ctypes.c_void_p(d), 0, 8, 8) == \
             N.LC_INVALID_VALUE
+    finally:
+        dev.close()
+
+
+def _free_device_bytes():
+    hip = ctypes.CDLL("libamdhip64.so")
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip.hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
+
+
+def test_no_alloc_allocates_nothing(lc, oracle):
+    lib = N.load()
+    dev = DeviceArrays(lib)
+    shapes = [(1000, 777, 1030),   # stream-K split tiles + padded copies of A and B
+              (512, 4096, 512),    # long K, whole tiles, no copies
+              (129, 64, 65)]       # padded copies of a small shape
+    try:
+        da = dev.alloc(1024 * 4096 * 4 + 16)
+        db = dev.alloc(4096 * 1030 * 4)
+        dc = dev.alloc(1024 * 1030 * 4)
+        inputs = []
+        for i, (m, k, n) in enumerate(shapes):
+            inputs.append((synth.uniform((m, k), stream=320 + 2 * i), synth.uniform((k, n), stream=321 + 2 * i)))
+        # warm-up: loads the module and takes the scratch symbol's address
+        a0, b0 = inputs[0]
+        _upload(lib, da, a0)
+        _upload(lib, db, b0)
+        m, k, n = shapes[0]
+        assert lib.lcMatMulDeviceNoAlloc(ctypes.c_void_p(da), ctypes.c_void_p(db), ctypes.c_void_p(dc),
+                                         m, k, n) == N.LC_SUCCESS
+        assert lib.lcDeviceSynchronize() == N.LC_SUCCESS
+        before = _free_device_bytes()
+        results = []
+        for (m, k, n), (a, b) in zip(shapes, inputs):
+            for off in (0, 4):  # aligned, then a base 4 bytes off (copied into the scratch)
+                note(f"[case] no-alloc memory check {m}x{k}x{n} offset {off}")
+                _upload(lib, da + off, a)
+                _upload(lib, db, b)
+                st = lib.lcMatMulDeviceNoAlloc(ctypes.c_void_p(da + off), ctypes.c_void_p(db),
+                                               ctypes.c_void_p(dc), m, k, n)
+                assert st == N.LC_SUCCESS, lib.lcGetLastErrorMessage().decode()
+                results.append(((m, k, n), off, _download(lib, dc, (m, n))))
+        after = _free_device_bytes()
+        assert after == before, f"free device memory moved by {before - after} bytes"
+        for (m, k, n), off, got in results:
+            a, b = inputs[shapes.index((m, k, n))]
+            assert_parity(oracle.matmul(a, b), got, "f32", f"no-alloc {m}x{k}x{n} offset {off}")
     finally:
         dev.close()
