@@ -63,9 +63,8 @@ def test_api_version_and_struct_sizes():
         assert lib.lcCheckStructSize(sid, ctypes.sizeof(st)) == 1
         assert lib.lcCheckStructSize(sid, ctypes.sizeof(st) + 4) == 0
     assert lib.lcGetStructSize(99) == 0
-    # sizes of the reference header's structs on x86-64 (gcc on
-    # include/lightning_core/lightning_core.h): 40 16 24 24 32 144
-    assert [lib.lcGetStructSize(i) for i in range(1, 7)] == [40, 16, 24, 24, 32, 144]
+    # the same sizes against the reference header itself, compiled with g++:
+    # tests/test_reference_binding.py::test_reference_struct_sizes_match_the_library
 
 
 def test_device_enum_appends_hip():
