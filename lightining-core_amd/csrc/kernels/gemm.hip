@@ -1711,20 +1711,32 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, 
   const int wm = (wave / WN) * (BM / WM);
   const int wn = (wave % WN) * (BN / WN);
 
-  // XCD-aware grouped tile order (as gemm_half_tn_lds_kernel).
+  // XCD-aware tile order.  Workgroup w runs on XCD w % 8, so the remap gives
+  // XCD x the contiguous range [x * n / 8, (x + 1) * n / 8) of the order
+  // below: the tile columns split into two halves and, within a half, tiles
+  // go row by row.  XCDs 0-3 then cover the first half's columns and XCDs
+  // 4-7 the second's, each about a quarter of the tile rows: an XCD's L2
+  // misses a quarter of A and half of B (one round of 156 workgroups in the
+  // ViT block's N = 768 GEMMs: 9.5 MB read from HBM per GEMM, where groups of
+  // 8 tile rows over every column read A about eight times, 14.7 MB).
   const int tiles_m = (M + BM - 1) / BM;
   const int full = static_cast<int>(gridDim.x) & ~7;
   int pid = blockIdx.x;
   if (pid < full) {
     pid = (pid & 7) * (full >> 3) + (pid >> 3);
   }
-  const int group_size = 8 * tiles_n;
-  const int group = pid / group_size;
-  const int first_m = group * 8;
-  const int gm = min(tiles_m - first_m, 8);
-  const int in_group = pid - group * group_size;
-  const int bm = (first_m + in_group % gm) * BM;
-  const int bn = (in_group / gm) * BN;
+  const int half_n = (tiles_n + 1) / 2;
+  const int first_half = tiles_m * half_n;
+  int bm, bn;
+  if (pid < first_half) {
+    bm = (pid / half_n) * BM;
+    bn = (pid % half_n) * BN;
+  } else {
+    const int rest = tiles_n - half_n;
+    const int q = pid - first_half;
+    bm = (q / rest) * BM;
+    bn = (half_n + q % rest) * BN;
+  }
 
   // Copy j of this wave is instruction i = wave + NW*j: A rows RPI*i ..
   // RPI*i + RPI-1 for j < A_LPW, else B rows RPI*(i - A_INS)..; lane l ->
