@@ -507,7 +507,7 @@ def bench_extras(lc, synth, cpu):
 # --pmc-workload`: the copy kernel behind a device-to-device lcMemcpy moves a
 # known number of bytes each way, which calibrates each counter; the GEMM's
 # per-dispatch means times those factors give its HBM traffic.  Figures from
-# profiles/gemm_f32_lds_kernel_1024_traffic.txt (update them when the kernel
+# profiles/gemm_f32_lds_kernel_1024cube_traffic.txt (update them when the kernel
 # changes).
 PMC_COPY_BYTES = 256 << 20
 PMC_COPIES = 10
@@ -516,9 +516,10 @@ PMC_GEMMS = 20
 # WRITE_SIZE: GEMM 4096.0 KiB/dispatch, copy 262144.0 KiB (x1.000).
 GEMM_F32_1024_TRAFFIC = 25235186 + 4194304  # HBM bytes per launch (fetch + write, calibrated)
 # 8192^3 bf16, HBM bytes per launch (fetch + write, calibrated), per kernel:
-# profiles/gemm_half_tn_w4r_kernel_8192cube_traffic.txt: FETCH_SIZE 787324.4 KiB/dispatch (x1.9998),
-# WRITE_SIZE 262144.0 KiB (x1.000).  A kernel without its own counter passes reports null.
-GEMM_BF16_8192_TRAFFIC = {"gemm_half_tn_w4r_kernel": 1612298878 + 268435462}
+# profiles/gemm_half_tn_w4h_kernel_8192cube_traffic.txt: FETCH_SIZE 788346.2 KiB/dispatch (x1.9998),
+# WRITE_SIZE 274117.1 KiB (x1.000).  A kernel without its own counter passes (a variant forced by
+# CJ_HIP_GEMM_TILE) reports null.
+GEMM_BF16_8192_TRAFFIC = {"gemm_half_tn_w4h_kernel": 1614381521 + 280695910}
 
 
 def pmc_workload(lc, synth, which="c2"):

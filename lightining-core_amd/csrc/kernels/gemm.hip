@@ -1717,8 +1717,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_half_ring_kernel(ASrc asrc, 
   // go row by row.  XCDs 0-3 then cover the first half's columns and XCDs
   // 4-7 the second's, each about a quarter of the tile rows: an XCD's L2
   // misses a quarter of A and half of B (one round of 156 workgroups in the
-  // ViT block's N = 768 GEMMs: 9.5 MB read from HBM per GEMM, where groups of
-  // 8 tile rows over every column read A about eight times, 14.7 MB).
+  // ViT block's N = 768 GEMMs: 11.4 MB read past L2 per GEMM, where groups
+  // of 8 tile rows over every column read A about eight times, 14.7 MB).
   const int tiles_m = (M + BM - 1) / BM;
   const int full = static_cast<int>(gridDim.x) & ~7;
   int pid = blockIdx.x;
