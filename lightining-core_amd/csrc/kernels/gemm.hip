@@ -241,7 +241,22 @@ struct LoadPatch {
 struct EpiF32 {
   float* C;
   int ldc;
+  int vec4 = 0;  // C is 16-byte aligned and ldc % 4 == 0 (store4 may use one 16-byte store)
   __device__ __forceinline__ void operator()(int m, int n, float v) const { C[static_cast<size_t>(m) * ldc + n] = v; }
+  // C[m][n .. n + 3] = v[0 .. 3] (n a multiple of 4), columns >= N dropped.
+  __device__ __forceinline__ void store4(int m, int n, int N, floatx4 v) const {
+    float* p = C + static_cast<size_t>(m) * ldc + n;
+    if (vec4 && n + 3 < N) {
+      *reinterpret_cast<floatx4*>(p) = v;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (n + r < N) {
+          p[r] = v[r];
+        }
+      }
+    }
+  }
 };
 
 template <typename T>
@@ -1436,7 +1451,10 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4r_kernel(const uint16_t* _
 // v_mfma_f32_16x16x32 (8 x 8 blocks of 16x16 per wave, 64 MFMAs per 32-deep
 // k-step): measured against the same schedule on 32x32x16 at 8192^3, 1463 vs
 // 1386 TFLOP/s on one box; the per-element k order is unchanged (results are
-// bit-identical to the other 256x256 kernels).  Copy j (0..3) of wave w for
+// bit-identical to the other 256x256 kernels).  The Bt fragment is the MFMAs'
+// A operand, so each lane accumulates 4 consecutive columns of one C row and
+// the epilogue stores 16 bytes per block (4096^3: 97.5 -> 96.0 us; 8192^3
+// unchanged).  Copy j (0..3) of wave w for
 // one part fills part rows 32w + 8j .. + 7: the four copies share one M0 and
 // step by the instruction offset.  The stage bodies are unrolled by five (the
 // ring's period), so every slot is a constant and every fragment read is one
@@ -1570,7 +1588,7 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* _
     // first half: k-step 0 on r0; r1 <- k-step 1; copies of parts 4s+8, 4s+9
 #pragma unroll
     for (int g = 0; g < 64; ++g) {
-      acc[g >> 3][g & 7] = mfma16x16x32<T>(r0[g >> 3], r0[8 + (g & 7)], acc[g >> 3][g & 7]);
+      acc[g >> 3][g & 7] = mfma16x16x32<T>(r0[8 + (g & 7)], r0[g >> 3], acc[g >> 3][g & 7]);
       __builtin_amdgcn_sched_barrier(0);
       if ((g & 1) == 0 && g < 32) {
         const int f = g >> 1;
@@ -1589,7 +1607,7 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* _
     // parts 4s+10, 4s+11
 #pragma unroll
     for (int g = 0; g < 64; ++g) {
-      acc[g >> 3][g & 7] = mfma16x16x32<T>(r1[g >> 3], r1[8 + (g & 7)], acc[g >> 3][g & 7]);
+      acc[g >> 3][g & 7] = mfma16x16x32<T>(r1[8 + (g & 7)], r1[g >> 3], acc[g >> 3][g & 7]);
       __builtin_amdgcn_sched_barrier(0);
       if ((g & 3) == 0) {
         const int f = g >> 2;
@@ -1611,17 +1629,17 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* _
   }
   wait_vmcnt<0>();  // no copy may still be writing LDS when the wave ends
 
+  // acc[i][j] holds rows i*16 + lane % 16 and columns j*16 + 4*(lane / 16) ..
+  // + 3 of the wave's C block (the MFMAs take the Bt fragment as their A
+  // operand, so they accumulate C^T): one 16-byte store per block.
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
+    const int m = bm + wm + i * 16 + lrow;
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int n = bn + wn + j * 16 + lrow;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = bm + wm + i * 16 + 4 * lq + r;
-        if (m < M && n < N) {
-          epi(m, n, acc[i][j][r]);
-        }
+      const int n = bn + wn + j * 16 + 4 * lq;
+      if (m < M) {
+        epi.store4(m, n, N, acc[i][j]);
       }
     }
   }
@@ -2349,8 +2367,9 @@ static hipError_t launch_gemm_w4(const uint16_t* A, const uint16_t* Bt, float* C
   const int tiles_n = (N + 255) / 256;
   const dim3 grid(((M + 255) / 256) * tiles_n);
   if constexpr (W4 == 3) {
+    const int vec4 = (ldc % 4 == 0 && reinterpret_cast<uintptr_t>(C) % 16 == 0) ? 1 : 0;
     hipLaunchKernelGGL((gemm_half_tn_w4h_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
-                       tiles_n, EpiF32{C, ldc});
+                       tiles_n, EpiF32{C, ldc, vec4});
   } else if constexpr (W4 == 2) {
     hipLaunchKernelGGL((gemm_half_tn_w4r_kernel<T, EpiF32>), grid, dim3(256), 0, stream, A, Bt, M, N, K, lda, ldb,
                        tiles_n, EpiF32{C, ldc});
