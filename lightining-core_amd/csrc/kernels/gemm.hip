@@ -1456,7 +1456,8 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4r_kernel(const uint16_t* _
 // the epilogue stores 16 bytes per block (4096^3: 97.5 -> 96.0 us; 8192^3
 // unchanged).  Copy j (0..3) of wave w for
 // one part fills part rows 32w + 8j .. + 7: the four copies share one M0 and
-// step by the instruction offset.  The stage bodies are unrolled by five (the
+// one SALU copy of the base pair, and step by the instruction offset.  The
+// stage bodies are unrolled by five (the
 // ring's period), so every slot is a constant and every fragment read is one
 // ds_read_b128 with an immediate offset from one of six lane bases.
 // Operands padded to 256 rows and K to 64; lane offsets are 32-bit (the host
@@ -1513,18 +1514,21 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* _
   const uint32_t wave_lds = lds_addr(smem) + static_cast<uint32_t>(wave) * 4096u;
   const int S = K / BK;
   // Copy j of part p (its stage clamped to the last: past the end a retired
-  // slot is refilled with the last stage, unused) into `slot`.
-  auto copy_pj = [&](int p, int slot, int j) {
+  // slot is refilled with the last stage, unused) into `slot`.  Copy 0 of a
+  // part makes the SALU copy of its base pair in `pair`; copies 1-3 read it.
+  auto copy_pj = [&](uint64_t& pair, int p, int slot, int j) {
     const int ty = p & 3;
-    const int st = min(p >> 2, S - 1);
-    const char* base = (ty < 2 ? a_tile : b_tile) + st * (BK * 2);
     const uint32_t voff = ty < 2 ? a_off[ty][j] : b_off[ty - 2][j];
     const uint32_t m0 = wave_lds + static_cast<uint32_t>(slot * PARTB);
     switch (j) {
-      case 0: load_lds16_sbase_off<0>(voff, base, m0); break;
-      case 1: load_lds16_sbase_off<1024>(voff, base, m0); break;
-      case 2: load_lds16_sbase_off<2048>(voff, base, m0); break;
-      default: load_lds16_sbase_off<3072>(voff, base, m0); break;
+      case 0: {
+        const int st = min(p >> 2, S - 1);
+        pair = load_lds16_sbase_first(voff, (ty < 2 ? a_tile : b_tile) + st * (BK * 2), m0);
+        break;
+      }
+      case 1: load_lds16_pair_off<1024>(voff, pair, m0); break;
+      case 2: load_lds16_pair_off<2048>(voff, pair, m0); break;
+      default: load_lds16_pair_off<3072>(voff, pair, m0); break;
     }
   };
 
@@ -1566,9 +1570,10 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* _
   // of stage 0 into registers.
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
+    uint64_t pair;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      copy_pj(p, p, j);
+      copy_pj(pair, p, p, j);
     }
   }
   wait_vmcnt<16>();                    // stage 0 has landed
@@ -1585,6 +1590,7 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* _
     constexpr int t = decltype(phase)::value;  // s % 5
     constexpr int sl0 = (4 * t) % NPART;       // slot of part 4s
     constexpr int nsl = (4 * t + 4) % NPART;   // slot of part 4s + 4
+    uint64_t pair = 0;                         // base pair of the part being copied
     // first half: k-step 0 on r0; r1 <- k-step 1; copies of parts 4s+8, 4s+9
 #pragma unroll
     for (int g = 0; g < 64; ++g) {
@@ -1596,7 +1602,7 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* _
       }
       if ((g & 7) == 4) {
         const int c = g >> 3;
-        copy_pj(4 * s + 8 + (c >> 2), (sl0 + 8 + (c >> 2)) % NPART, c & 3);
+        copy_pj(pair, 4 * s + 8 + (c >> 2), (sl0 + 8 + (c >> 2)) % NPART, c & 3);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -1615,7 +1621,7 @@ __global__ __launch_bounds__(256) void gemm_half_tn_w4h_kernel(const uint16_t* _
       }
       if ((g & 7) == 4) {
         const int c = g >> 3;
-        copy_pj(4 * s + 10 + (c >> 2), (sl0 + 10 + (c >> 2)) % NPART, c & 3);
+        copy_pj(pair, 4 * s + 10 + (c >> 2), (sl0 + 10 + (c >> 2)) % NPART, c & 3);
       }
       __builtin_amdgcn_sched_barrier(0);
     }

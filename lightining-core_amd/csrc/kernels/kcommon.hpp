@@ -184,6 +184,32 @@ __device__ __forceinline__ void load_lds16_sbase_off(uint32_t voff, const void* 
                : "memory");
 }
 
+// The first of several copies that share one base (and one M0 value): the
+// asm copies the base pair with an SALU move, as load_lds16_sbase_off does,
+// issues the copy at instruction offset 0 and returns the pair it copied, so
+// the copies after it (load_lds16_pair_off) read an SGPR pair whose last
+// writer is that SALU move.  One move per part instead of one per copy
+// (measured on the 8192^3 bf16 GEMM: 12 fewer SALU instructions per stage,
+// 1531 -> 1562 TFLOP/s).  The hazard scan in tests/test_asm_hazards.py checks
+// the built code for VALU writes of the pair within 5 wait states of a copy.
+__device__ __forceinline__ uint64_t load_lds16_sbase_first(uint32_t voff, const void* sbase, uint32_t lds) {
+  uint64_t pair;
+  asm volatile("s_mov_b64 %0, %2\n\tglobal_load_lds_dwordx4 %1, %0"
+               : "=&s"(pair)
+               : "v"(voff), "s"(sbase), "{m0}"(lds)
+               : "memory");
+  return pair;
+}
+
+// A later copy of the same base pair and M0 value at instruction offset OFF
+// (M0 must not change between the first copy and this one: the compiler
+// keeps it, since every copy names the same value as its "{m0}" input).
+template <int OFF>
+__device__ __forceinline__ void load_lds16_pair_off(uint32_t voff, uint64_t pair, uint32_t lds) {
+  static_assert(OFF > 0 && OFF < 4096, "instruction offset");
+  asm volatile("global_load_lds_dwordx4 %0, %1 offset:%2" : : "v"(voff), "s"(pair), "i"(OFF), "{m0}"(lds) : "memory");
+}
+
 // LDS byte address of a __shared__ object, as a wave-uniform value.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p)));

@@ -1,16 +1,25 @@
 """Hardware-hazard scan of the built gfx950 kernels (CPU only: hipcc -S).
 
-The global -> LDS copies are inline asm (kcommon.hpp, load_lds16_sbase), and
-the compiler does not pad the inside of an asm statement for hazards.  Two
-apply to these copies (AMD CDNA3/CDNA4 ISA, "manually inserted wait states"):
+The global -> LDS copies are inline asm (kcommon.hpp, load_lds16_sbase and
+its variants), and the compiler does not pad the inside of an asm statement
+for hazards.  Two apply to these copies (AMD CDNA3/CDNA4 ISA, "manually
+inserted wait states"):
 
 * a VALU write of an SGPR needs 5 wait states before a VMEM instruction reads
   that SGPR.  The copy's 64-bit base may arrive straight from a v_readlane
   (a spilled SGPR reloaded by the compiler): one wait state after it, a copy
   took a stale half of its base and faulted the GPU.  The asm therefore reads
-  an SALU copy of the base made by its first instruction;
+  an SALU copy of the base made by its first instruction, or (several copies
+  of one part) an SALU copy made by the first copy's asm earlier in the same
+  basic block;
 * an SALU write of M0 needs 1 wait state before an LDS-DMA load reads M0
-  (the SALU copy above is that wait state); a VALU write of M0 would need 5.
+  (the SALU copy above is that wait state for a part's first copy; later
+  copies reuse M0); a VALU write of M0 would need 5.
+
+The scan applies the rules themselves: for every LDS-DMA load, each SGPR of
+its base pair must have been last written, in the same basic block, by an
+SALU instruction, and no VALU write of it may lie within 5 wait states; the
+instruction right before the load must not write M0, and no VALU writes M0.
 
 A third check covers a second fault of the same family, in host-visible
 kernel code rather than the asm: a 64-bit base rebuilt from a 32-bit
@@ -91,10 +100,18 @@ def _sign_extended_readfirstlane_base(ins, i, pair):
     return k is not None and ins[k].startswith("v_readfirstlane_b32")
 
 
+def _wait_states(t):
+    """Wait states an instruction provides (s_nop N: N + 1)."""
+    m = re.match(r"^s_nop\s+(\d+)", t)
+    return int(m.group(1)) + 1 if m else 1
+
+
 def scan(text):
-    """Problems found: LDS-DMA loads whose SGPR base is not an SALU copy made
-    by the instruction right before, bases whose high half is a sign-extended
-    v_readfirstlane result, and VALU writes of M0."""
+    """Problems found: LDS-DMA loads whose SGPR base was last written by a
+    VALU instruction (or by anything outside the load's basic block), VALU
+    writes of a base SGPR within 5 wait states of a load, M0 written by the
+    instruction right before a load, VALU writes of M0, and bases whose high
+    half is a sign-extended v_readfirstlane result."""
     problems = []
     ins = _instructions(text)
     for i, t in enumerate(ins):
@@ -104,14 +121,31 @@ def scan(text):
         if not m:
             continue
         base = m.group(1)
-        prev = ins[i - 1] if i > 0 else ""
-        pm = re.match(r"^s_mov_b64\s+(s\[\d+:\d+\]),\s*(s\[\d+:\d+\])$", prev)
-        if not pm or pm.group(1) != base:
-            problems.append(f"load reads {base} not copied by the previous SALU move: [{prev}] -> [{t}]")
-            src = base
+        if i > 0 and "m0" in _dest(ins[i - 1]):
+            problems.append(f"M0 written with no wait state before the load: [{ins[i - 1]}] -> [{t}]")
+        # the last writer of each half, in this basic block, is an SALU
+        # instruction (a VALU one is also reported when it lies within 5 wait
+        # states, the faulting case)
+        writers = set()
+        for reg in sorted(_sregs(base)):
+            j = _last_writer(ins, i, reg)
+            if j is None:
+                problems.append(f"load base {reg} not written in the load's basic block: [{t}]")
+            elif not ins[j].startswith("s_"):
+                ws = sum(_wait_states(x) for x in ins[j + 1:i])
+                if ws < 5:
+                    problems.append(f"VALU write of {reg} {ws} wait states before the load: [{ins[j]}] -> [{t}]")
+                problems.append(f"load base {reg} last written by a non-SALU instruction: [{ins[j]}] -> [{t}]")
+            else:
+                writers.add(j)
+        # a base copied by s_mov_b64: check where the copy came from
+        if len(writers) == 1:
+            j = writers.pop()
+            pm = re.match(r"^s_mov_b64\s+(s\[\d+:\d+\]),\s*(s\[\d+:\d+\])$", ins[j])
+            src, at = (pm.group(2), j) if pm and pm.group(1) == base else (base, i)
         else:
-            src = pm.group(2)
-        if _sign_extended_readfirstlane_base(ins, i - 1 if pm else i, src):
+            src, at = base, i
+        if _sign_extended_readfirstlane_base(ins, at, src):
             problems.append(f"load base {src} is a sign-extended v_readfirstlane value: [{t}]")
     return problems
 
@@ -136,10 +170,40 @@ def test_scan_catches_the_faulting_sequence():
         "\tglobal_load_lds_dwordx4 v195, s[6:7]",
         "\t;;#ASMEND",
     ])
-    assert len(scan(planted)) == 1
+    found = scan(planted)
+    assert any("VALU write of s7 1 wait states" in f for f in found), found
     fixed = planted.replace("s_nop 0", "s_mov_b64 s[40:41], s[6:7]").replace("v195, s[6:7]", "v195, s[40:41]")
     assert scan(fixed) == []
     assert scan("\tv_readfirstlane_b32 m0, v3\n") != []
+
+
+def test_scan_accepts_a_shared_salu_copy_and_catches_a_bare_m0_write():
+    # the copies of one part: the first asm copies the base, the next read the copy
+    shared = "\n".join([
+        "\ts_add_u32 s2, s4, s33",
+        "\ts_addc_u32 s3, s5, s34",
+        "\ts_mov_b32 m0, s27",
+        "\ts_mov_b64 s[36:37], s[2:3]",
+        "\tglobal_load_lds_dwordx4 v64, s[36:37]",
+        "\tv_mfma_f32_16x16x32_bf16 a[0:3], v[0:3], v[4:7], a[0:3]",
+        "\tglobal_load_lds_dwordx4 v68, s[36:37] offset:1024",
+        "\tds_read_b128 v[8:11], v85 offset:2048",
+        "\tglobal_load_lds_dwordx4 v72, s[36:37] offset:2048",
+    ])
+    assert scan(shared) == []
+    # M0 rewritten right before a later copy: no wait state
+    bare_m0 = shared.replace("\tglobal_load_lds_dwordx4 v72", "\ts_mov_b32 m0, s28\n\tglobal_load_lds_dwordx4 v72")
+    found = scan(bare_m0)
+    assert len(found) == 1 and "M0" in found[0], found
+    # the shared copy reloaded by the compiler between the copies (a spill)
+    reload = shared.replace("\tds_read_b128 v[8:11], v85 offset:2048",
+                            "\tv_readlane_b32 s36, v200, 3\n\ts_nop 1")
+    found = scan(reload)
+    assert any("VALU write" in f for f in found) and any("non-SALU" in f for f in found), found
+    # ... or a base that reaches the copy across a label
+    merged = shared.replace("\tv_mfma_f32_16x16x32_bf16", ".LBB0_7:\n\tv_mfma_f32_16x16x32_bf16")
+    found = scan(merged)
+    assert len(found) == 4 and all("basic block" in f for f in found), found  # two loads, two halves each
 
 
 def test_scan_catches_a_sign_extended_readfirstlane_base():
