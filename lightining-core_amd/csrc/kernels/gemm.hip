@@ -2265,8 +2265,9 @@ __global__ __launch_bounds__(256 * KS) void gemm_f32_lds_kernel(const float* __r
 // Default: the largest tile that still gives at least one workgroup per CU
 // (w4h from one tile per CU where the operands are padded, big8 elsewhere).
 // Alternating runs on one box, 8192^3 / 4096^3 bf16 TFLOP/s: w4h 1516-1529 /
-// 1464-1467, w4r 1387-1390 / 1302-1307.
-// Measured with alternating runs on one box, 8192^3 / 4096^3 bf16 TFLOP/s:
+// 1464-1467, w4r 1387-1390 / 1302-1307 (w4h since: 16-byte C stores and one
+// base copy per part, 1555 / 1514 against w4r 1393 / 1319 on another box).
+// Earlier, with alternating runs on one box, 8192^3 / 4096^3 bf16 TFLOP/s:
 // w4r 1281-1299 / 1271-1280, w4d 1287-1299 / 1263-1269, w4 1281-1289 /
 // 1203-1204; w4r also takes 3.5% fewer cycles at 8192^3 in the counters
 // (half the L2 read requests of w4, L2 latency 268 against 323 cycles).
