@@ -106,10 +106,13 @@ int attentionF32Splits(int bh, int S, int D, int requested);
 // ReLU) of x [batch, cin, h, wd] with w [cout, cin, kh, kw], Q/K/V = the
 // consecutive S*D slices of its flat output repeated to 3*S*D values, then
 // single-head non-causal attention -> out [S, D].  The conv output must have
-// at most 8192 values.
+// at most 8192 values.  With done_flag (host-mapped) and done_count (device,
+// zero), the launch's last workgroup writes done_seq to *done_flag once every
+// workgroup's output is visible to the host, and leaves the counter at zero.
 hipError_t convAttentionF32(const float* x, const float* w, const float* bias, int batch, int cin, int h, int wd,
                             int cout, int kh, int kw, int sh, int sw, int ph, int pw, int S, int D, float* out,
-                            hipStream_t stream);
+                            hipStream_t stream, unsigned* done_count = nullptr, unsigned* done_flag = nullptr,
+                            unsigned done_seq = 0);
 // True when convAttentionF32 reads x, w and bias exactly once per workgroup
 // (all staged in LDS): then they may live in mapped host memory.
 bool convAttentionStagesInputs(int batch, int cin, int h, int wd, int cout, int kh, int kw, int sh, int sw, int ph,

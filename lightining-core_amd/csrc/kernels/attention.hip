@@ -54,6 +54,8 @@ struct AttnSrcGlobal {
   __device__ Pos fwd(Pos p, size_t d) const { return p + d; }
   template <int W>
   __device__ float ld(const float*, Pos p) const { return (W == 0 ? q : W == 1 ? k : v)[p]; }
+  __device__ bool single_writer() const { return false; }
+  __device__ void finish() const {}
 };
 
 // The reference's conv -> attention chain (bind_integrated.cpp:614-730):
@@ -71,6 +73,11 @@ struct AttnSrcConvRepeat {
   int n;        // conv output values (batch * cout * oh * ow), at most kOut
   int xs, ws;   // input and weight values
   size_t need;  // S * D
+  // Optional completion flag (host-mapped): after every workgroup's output is
+  // visible to the host, the last one writes done_seq into *done_flag.
+  unsigned* done_count = nullptr;
+  unsigned* done_flag = nullptr;
+  unsigned done_seq = 0;
   static constexpr int kOut = 8192;
   static constexpr int kLds = 12288;
   static constexpr bool kVec = false;
@@ -212,6 +219,29 @@ struct AttnSrcConvRepeat {
   }
   template <int W>
   __device__ float ld(const float* buf, Pos p) const { return buf[p]; }
+  // With a completion flag, wave 0 stores the workgroup's whole output
+  // (single_writer), so one wave's system-scope release covers it.
+  __device__ bool single_writer() const { return done_flag != nullptr; }
+  // Called by every thread after the output stores.  Wave 0 makes its stores
+  // visible to the host (system-scope release), then thread 0 counts the
+  // workgroup (acquire-release at device scope, so the last workgroup's
+  // count follows every other workgroup's release); the last workgroup zeroes
+  // the counter for the next call and publishes the sequence number with a
+  // system-scope release store.
+  __device__ void finish() const {
+    if (done_flag == nullptr || threadIdx.x >= 64) {
+      return;
+    }
+    __threadfence_system();
+    if (threadIdx.x == 0) {
+      const unsigned total = gridDim.x * gridDim.y * gridDim.z;
+      if (__hip_atomic_fetch_add(done_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == total - 1) {
+        __hip_atomic_store(done_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __threadfence_system();
+        __hip_atomic_store(done_flag, done_seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+      }
+    }
+  }
 };
 
 // Fills rows row0, row0 + rstep, ... (< ROWS) of ROWS x DP tiles (row stride
@@ -508,15 +538,19 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
   // rows w, w + KS, ..., its lanes over the columns.
   const int rows = min(32, S - q0);
   float* dst = out + static_cast<size_t>(q0) * D;
-  for (int r = wave; r < rows; r += KS) {
+  const bool one = src.single_writer();
+  if (!one || wave == 0) {
+    for (int r = one ? 0 : wave; r < rows; r += one ? 1 : KS) {
 #pragma unroll
-    for (int c0 = 0; c0 < DP; c0 += 64) {
-      const int c = c0 + lane;
-      if (c < D) {
-        dst[r * D + c] = tile[r * TS + c];
+      for (int c0 = 0; c0 < DP; c0 += 64) {
+        const int c = c0 + lane;
+        if (c < D) {
+          dst[r * D + c] = tile[r * TS + c];
+        }
       }
     }
   }
+  src.finish();
 }
 
 // ---------------------------------------------------------------------------
@@ -757,11 +791,15 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_q16_kernel(Src src, floa
   // Rows q0 .. q0 + rows - 1 are one contiguous range of out.
   const int rows = min(16, S - q0);
   float* dst = out + head + static_cast<size_t>(q0) * D;
-  for (int r = wave; r < rows; r += KS) {
-    if (lane < D) {
-      dst[r * D + lane] = tile[r * TS + lane];
+  const bool one = src.single_writer();
+  if (!one || wave == 0) {
+    for (int r = one ? 0 : wave; r < rows; r += one ? 1 : KS) {
+      if (lane < D) {
+        dst[r * D + lane] = tile[r * TS + lane];
+      }
     }
   }
+  src.finish();
 }
 
 // ---------------------------------------------------------------------------
@@ -1999,7 +2037,7 @@ bool convAttentionStagesInputs(int batch, int cin, int h, int wd, int cout, int 
 
 hipError_t convAttentionF32(const float* x, const float* w, const float* bias, int batch, int cin, int h, int wd,
                             int cout, int kh, int kw, int sh, int sw, int ph, int pw, int S, int D, float* out,
-                            hipStream_t stream) {
+                            hipStream_t stream, unsigned* done_count, unsigned* done_flag, unsigned done_seq) {
   const int oh = (h + 2 * ph - kh) / sh + 1;
   const int ow = (wd + 2 * pw - kw) / sw + 1;
   const long long n = static_cast<long long>(batch) * cout * oh * ow;
@@ -2013,6 +2051,9 @@ hipError_t convAttentionF32(const float* x, const float* w, const float* bias, i
   AttnSrcConvRepeat src{x, w, bias, cin, h, wd, cout, kh, kw, sh, sw, ph, pw, oh, ow, static_cast<int>(n),
                         static_cast<int>(xs < big ? xs : big), static_cast<int>(ws < big ? ws : big),
                         static_cast<size_t>(S) * D};
+  src.done_count = done_count;
+  src.done_flag = done_flag;
+  src.done_seq = done_seq;
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
   // D <= 64: the 16-query kernel (16 waves of 16-key tiles, 8 at D > 48 so
   // that the per-wave tiles fit next to the conv buffer).

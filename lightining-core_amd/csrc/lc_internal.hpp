@@ -142,6 +142,14 @@ struct HipContext {
   // family (noteEnqueued; syncStream resets both).
   std::size_t matmul_inflight = 0;
   std::size_t attention_inflight = 0;
+  // Completion flag of a synchronous small call (waitDoneFlag): the last
+  // workgroup of its kernel writes the call's sequence number into done_flag
+  // (pinned, device-mapped) after every workgroup's results are visible to
+  // the host; done_count (device) counts the finished workgroups and is left
+  // at zero by the last one.
+  PinnedBuffer done_flag;
+  DeviceBuffer done_count;
+  unsigned done_seq = 0;
 };
 
 bool hipAvailable();
@@ -155,6 +163,15 @@ Status download(HipContext* ctx, void* dst, const void* src, std::size_t bytes);
 // Synchronises the backend stream, then reports a failure a kernel recorded
 // since the last sync (a stream-K wait that ran out) as kDriverError.
 Status syncStream(HipContext* ctx);
+// The completion flag for the next synchronous small call: allocates it once,
+// returns its device alias, the device counter and the call's sequence number.
+Status prepareDoneFlag(HipContext* ctx, unsigned** flag_dev, unsigned** count_dev, unsigned* seq);
+// Waits for a kernel launched with the flag from prepareDoneFlag to report
+// `seq` by spinning on the pinned word (a stream sync costs ~5 us more), then
+// does syncStream's bookkeeping.  If the word does not arrive within the
+// limit, falls back to syncStream (which reports any launch failure) and
+// re-zeroes the counter.
+Status waitDoneFlag(HipContext* ctx, unsigned seq);
 // Bookkeeping of enqueue-only launches (no download, no synchronize), as the
 // reference's backends cap their in-flight submissions: matmul at 256
 // (src/ops/matmul_metal.mm:27, :1864-1878, :1969-1973, :2066-2070),

@@ -256,8 +256,10 @@ Status download(HipContext* ctx, void* dst, const void* src, std::size_t bytes) 
   return Status::kSuccess;
 }
 
-Status syncStream(HipContext* ctx) {
-  LC_HIP_TRY(hipStreamSynchronize(ctx->stream));
+namespace {
+// Bookkeeping after the stream has drained: in-flight counts restart, and a
+// failure a kernel recorded since the last sync becomes an error.
+Status afterSync(HipContext* ctx) {
   ctx->matmul_inflight = 0;
   ctx->attention_inflight = 0;
   if (int* word = static_cast<int*>(ctx->gemm_fail.get())) {
@@ -274,6 +276,49 @@ Status syncStream(HipContext* ctx) {
                   "matmul: a stream-K workgroup's bounded wait for a partial tile ran out "
                   "(CJ_HIP_STREAMK_SPIN_LIMIT); the result of that launch is invalid");
     }
+  }
+  return Status::kSuccess;
+}
+}  // namespace
+
+Status syncStream(HipContext* ctx) {
+  LC_HIP_TRY(hipStreamSynchronize(ctx->stream));
+  return afterSync(ctx);
+}
+
+Status prepareDoneFlag(HipContext* ctx, unsigned** flag_dev, unsigned** count_dev, unsigned* seq) {
+  if (ctx->done_flag.get() == nullptr) {
+    LC_TRY(ctx->done_flag.ensure(64));
+    __atomic_store_n(static_cast<unsigned*>(ctx->done_flag.get()), 0u, __ATOMIC_RELEASE);
+    LC_TRY(ctx->done_count.ensure(64, true));
+    LC_HIP_TRY(hipStreamSynchronize(ctx->stream));  // the zeroed counter is in place
+  }
+  ctx->done_seq = ctx->done_seq + 1 == 0 ? 1 : ctx->done_seq + 1;  // never 0, the initial word
+  *flag_dev = static_cast<unsigned*>(ctx->done_flag.device());
+  *count_dev = ctx->done_count.as<unsigned>();
+  *seq = ctx->done_seq;
+  return Status::kSuccess;
+}
+
+Status waitDoneFlag(HipContext* ctx, unsigned seq) {
+  const unsigned* word = static_cast<const unsigned*>(ctx->done_flag.get());
+  const auto t0 = std::chrono::steady_clock::now();
+  for (;;) {
+    if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == seq) {
+      return afterSync(ctx);
+    }
+    if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(200)) {
+      break;
+    }
+  }
+  // Not seen in time: the stream sync reports a failed launch; after one
+  // that completed, its results are in place whether or not the word came
+  // (a counter left off zero by an earlier failed launch keeps it away), so
+  // the counter is re-zeroed for the next call.
+  LC_TRY(syncStream(ctx));
+  if (__atomic_load_n(word, __ATOMIC_ACQUIRE) != seq) {
+    LC_HIP_TRY(hipMemsetAsync(ctx->done_count.get(), 0, ctx->done_count.size(), ctx->stream));
+    LC_HIP_TRY(hipStreamSynchronize(ctx->stream));
   }
   return Status::kSuccess;
 }

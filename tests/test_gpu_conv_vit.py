@@ -69,6 +69,7 @@ def test_conv_extra(lc, oracle, xs, ws, stride, pad):
     ((1, 4, 12, 10), (7, 4, 3, 3), (1, 1), (0, 0), 33, 20),
     ((1, 4, 64, 64), (8, 4, 3, 3), (4, 4), (1, 1), 64, 32),
     ((1, 5, 8, 8), (16, 5, 3, 3), (1, 1), (1, 1), 48, 48),
+    ((1, 3, 8, 8), (16, 3, 3, 3), (1, 1), (1, 1), 40, 100),
 ])
 def test_conv_attention_shapes(lc, oracle, xs, ws, stride, pad, seq, hd):
     x, w = synth.normal(xs, stream=40), synth.normal(ws, std=0.3, stream=41)
@@ -76,6 +77,25 @@ def test_conv_attention_shapes(lc, oracle, xs, ws, stride, pad, seq, hd):
     got = lc.api.conv_attention_torchstrong_nchw(x, w, bias, seq, hd, stride[0], stride[1], pad[0], pad[1])
     ref = oracle.conv_attention(x, w, bias, seq, hd, stride, pad)
     assert_parity(ref.ravel(), got, "f32", f"conv_attention {xs} {ws} seq={seq} d={hd}")
+
+
+# The fused calls return when their kernel's last workgroup raises a
+# host-mapped completion flag (no stream sync).  Back-to-back calls with
+# fresh inputs, cycling through shapes of both fused kernels (16-query D <= 64,
+# 32-query D > 64) and both execution modes, must each return the result of
+# their own inputs: an output read before the kernel's stores were visible
+# would show the previous call's values.
+def test_conv_attention_repeated_calls_see_their_own_results(lc, oracle):
+    shapes = [(48, 48), (192, 8), (40, 100), (96, 48)]
+    for it in range(48):
+        seq, hd = shapes[it % len(shapes)]
+        mode = "eager" if (it // len(shapes)) % 2 == 0 else "graph"
+        x = synth.normal((1, 3, 8, 8), stream=700 + it)
+        w = synth.normal((16, 3, 3, 3), std=0.3, stream=800 + it)
+        bias = synth.normal((16,), stream=900 + it)
+        got = lc.api.conv_attention_torchstrong_nchw(x, w, bias, seq, hd, 1, 1, 1, 1, execution_mode=mode)
+        ref = oracle.conv_attention(x, w, bias, seq, hd, (1, 1), (1, 1))
+        assert_parity(ref.ravel(), got, "f32", f"call {it} {mode} seq={seq} d={hd}")
 
 
 # Graph mode: one HIP graph per shape key, replayed.  Each case replays it four
