@@ -234,6 +234,67 @@ Status trainSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, cons
   return Status::kSuccess;
 }
 
+// Small one-head fp32 calls that upload every input and download the output
+// (the plain attention2d call) spend most of their time in per-copy
+// overhead: three pageable uploads, a pageable download and a stream sync,
+// ~10 us each at 64 KB.  Here the inputs are packed into pinned staging and
+// one copy kernel reads them through its device alias into the resident
+// buffers (a DMA copy from pinned memory still costs ~10 us per copy at these
+// sizes); the attention kernel writes the output straight into the staging
+// and raises the host-mapped completion flag, which the call waits for
+// instead of a stream sync.
+constexpr std::size_t kQuickAttnElems = std::size_t{1} << 16;  // S * D per tensor
+
+bool quickAttnEnabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("CJ_HIP_ATTN_QUICK");
+    return v == nullptr || std::string(v) != "0";
+  }();
+  return on;
+}
+
+Status attentionForwardQuick(HipContext* ctx, AttnResident& res, const AttnShape& sh, const float* q,
+                             const float* k, const float* v, float* out, const lcAttentionIoPolicy& policy) {
+  const std::size_t n = sh.elems();
+  const std::size_t bytes = n * sizeof(float);
+  const std::size_t out_at = roundUp(3 * n, 64);  // 256-byte aligned output
+  LC_TRY(ctx->pinned.ensure((out_at + n) * sizeof(float)));
+  LC_TRY(res.q.ensure(bytes));
+  LC_TRY(res.k.ensure(bytes));
+  LC_TRY(res.v.ensure(bytes));
+  LC_TRY(res.out.ensure(bytes));
+  float* stage = static_cast<float*>(ctx->pinned.get());
+  std::memcpy(stage, q, bytes);
+  std::memcpy(stage + n, k, bytes);
+  std::memcpy(stage + 2 * n, v, bytes);
+  const hipError_t ce = kern::split3CopyF32(static_cast<const float*>(ctx->pinned.device()), res.q.as<float>(),
+                                            res.k.as<float>(), res.v.as<float>(), n, ctx->stream);
+  if (ce != hipSuccess) {
+    return failHip(ce, "attention input copy");
+  }
+  res.has_q = res.has_k = res.has_v = true;
+  int splits = 0;
+  LC_TRY(forwardSplits(ctx, res, sh, policy, &splits));
+  unsigned* flag_dev = nullptr;
+  unsigned* count_dev = nullptr;
+  unsigned seq = 0;
+  LC_TRY(prepareDoneFlag(ctx, &flag_dev, &count_dev, &seq));
+  const int S = static_cast<int>(sh.seq_len);
+  const int D = static_cast<int>(sh.head_dim);
+  traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, sh.seq_len * sh.seq_len * sh.head_dim);
+  const hipError_t e = kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(),
+                                          static_cast<float*>(ctx->pinned.device()) + out_at, 1, S, D, sh.causal,
+                                          policy.output_scale, policy.output_bias, policy.output_relu, nullptr,
+                                          ctx->stream, splits, count_dev, flag_dev, seq);
+  if (e != hipSuccess) {
+    return failHip(e, "attention kernel launch");
+  }
+  LC_TRY(waitDoneFlag(ctx, seq));
+  std::memcpy(out, stage + out_at, bytes);
+  res.has_out = false;  // the output went to the staging, not to res.out
+  return Status::kSuccess;
+}
+
 }  // namespace
 
 Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnShape& sh, const float* q,
@@ -264,6 +325,10 @@ Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnSh
   }
 
   const bool half = isHalf(sh.dtype);
+  if (!half && sh.bh() == 1 && repeat == 1 && policy.upload_q && policy.upload_k && policy.upload_v &&
+      policy.download_out && sh.elems() <= kQuickAttnElems && quickAttnEnabled()) {
+    return attentionForwardQuick(ctx, res, sh, q, k, v, out, policy);
+  }
   if (policy.upload_q) {
     LC_TRY(uploadAttnTensor(ctx, res, sh, q, res.q, false));
     res.has_q = true;

@@ -68,6 +68,15 @@ hipError_t gemmF32ConvNchw(const float* cols, const float* Wt, float* out, int M
 // row = (n*oh + oy)*ow + ox, col = (c*kh + ky)*kw + kx.
 hipError_t im2colF32(const float* x, float* cols, int batch, int C, int H, int W, int kh, int kw, int sh, int sw,
                      int ph, int pw, int oh, int ow, hipStream_t stream);
+// d0 / d1 / d2 [0, n) = src [0, n) / [n, 2n) / [2n, 3n); src may be the device
+// alias of pinned host memory (read once).
+hipError_t split3CopyF32(const float* src, float* d0, float* d1, float* d2, size_t n, hipStream_t stream);
+// dst [0, n) = src [0, n), dst being the device alias of pinned host memory;
+// then the launch's last workgroup writes done_seq to *done_flag (host-mapped)
+// once every value is visible to the host, and leaves *done_count (device,
+// zero) at zero.
+hipError_t copyOutFlagF32(const float* src, float* dst, size_t n, unsigned* done_count, unsigned* done_flag,
+                          unsigned done_seq, hipStream_t stream);
 // Fills dst with the first `total` floats of the infinite repetition of src[0:n].
 hipError_t repeatFillF32(const float* src, size_t n, float* dst, size_t total, hipStream_t stream);
 
@@ -88,7 +97,8 @@ hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu,
 // log2 domain (p = exp2((q.k)*scale*log2(e) - m) / l).
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D,
                         bool causal, float post_scale, float post_bias, int post_relu, float* stats,
-                        hipStream_t stream, int splits = 0);
+                        hipStream_t stream, int splits = 0, unsigned* done_count = nullptr,
+                        unsigned* done_flag = nullptr, unsigned done_seq = 0);
 // The `splits` value that selects the 16-query fp32 forward kernel
 // (attn_fwd_f32_q16_kernel: 16 waves of 16-key tiles per 16 queries), for
 // problems too small to fill the GPU.  Needs D <= 64, D % 4 == 0 and 16-byte
@@ -108,7 +118,8 @@ int attentionF32Splits(int bh, int S, int D, int requested);
 // single-head non-causal attention -> out [S, D].  The conv output must have
 // at most 8192 values.  With done_flag (host-mapped) and done_count (device,
 // zero), the launch's last workgroup writes done_seq to *done_flag once every
-// workgroup's output is visible to the host, and leaves the counter at zero.
+// workgroup's output is visible to the host, and leaves the counter at zero
+// (attentionF32 takes the same optional flag, without stats).
 hipError_t convAttentionF32(const float* x, const float* w, const float* bias, int batch, int cin, int h, int wd,
                             int cout, int kh, int kw, int sh, int sw, int ph, int pw, int S, int D, float* out,
                             hipStream_t stream, unsigned* done_count = nullptr, unsigned* done_flag = nullptr,

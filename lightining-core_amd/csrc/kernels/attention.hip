@@ -42,6 +42,7 @@ struct AttnSrcGlobal {
   const float* q;
   const float* k;
   const float* v;
+  DoneFlag done{};
   static constexpr int kLds = 0;
   static constexpr bool kVec = true;
   static constexpr bool kClamp = false;  // padding cells are not loaded
@@ -54,8 +55,8 @@ struct AttnSrcGlobal {
   __device__ Pos fwd(Pos p, size_t d) const { return p + d; }
   template <int W>
   __device__ float ld(const float*, Pos p) const { return (W == 0 ? q : W == 1 ? k : v)[p]; }
-  __device__ bool single_writer() const { return false; }
-  __device__ void finish() const {}
+  __device__ bool single_writer() const { return done.single_writer(); }
+  __device__ void finish() const { done.finish(); }
 };
 
 // The reference's conv -> attention chain (bind_integrated.cpp:614-730):
@@ -73,11 +74,7 @@ struct AttnSrcConvRepeat {
   int n;        // conv output values (batch * cout * oh * ow), at most kOut
   int xs, ws;   // input and weight values
   size_t need;  // S * D
-  // Optional completion flag (host-mapped): after every workgroup's output is
-  // visible to the host, the last one writes done_seq into *done_flag.
-  unsigned* done_count = nullptr;
-  unsigned* done_flag = nullptr;
-  unsigned done_seq = 0;
+  DoneFlag done{};  // optional completion flag
   static constexpr int kOut = 8192;
   static constexpr int kLds = 12288;
   static constexpr bool kVec = false;
@@ -219,29 +216,8 @@ struct AttnSrcConvRepeat {
   }
   template <int W>
   __device__ float ld(const float* buf, Pos p) const { return buf[p]; }
-  // With a completion flag, wave 0 stores the workgroup's whole output
-  // (single_writer), so one wave's system-scope release covers it.
-  __device__ bool single_writer() const { return done_flag != nullptr; }
-  // Called by every thread after the output stores.  Wave 0 makes its stores
-  // visible to the host (system-scope release), then thread 0 counts the
-  // workgroup (acquire-release at device scope, so the last workgroup's
-  // count follows every other workgroup's release); the last workgroup zeroes
-  // the counter for the next call and publishes the sequence number with a
-  // system-scope release store.
-  __device__ void finish() const {
-    if (done_flag == nullptr || threadIdx.x >= 64) {
-      return;
-    }
-    __threadfence_system();
-    if (threadIdx.x == 0) {
-      const unsigned total = gridDim.x * gridDim.y * gridDim.z;
-      if (__hip_atomic_fetch_add(done_count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == total - 1) {
-        __hip_atomic_store(done_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __threadfence_system();
-        __hip_atomic_store(done_flag, done_seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-      }
-    }
-  }
+  __device__ bool single_writer() const { return done.single_writer(); }
+  __device__ void finish() const { done.finish(); }
 };
 
 // Fills rows row0, row0 + rstep, ... (< ROWS) of ROWS x DP tiles (row stride
@@ -1962,8 +1938,9 @@ int attentionF32Splits(int bh, int S, int D, int requested) {
 
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D, bool causal,
                         float post_scale, float post_bias, int post_relu, float* stats, hipStream_t stream,
-                        int splits) {
-  if (D <= 0 || D > 256 || S <= 0 || bh <= 0) {
+                        int splits, unsigned* done_count, unsigned* done_flag, unsigned done_seq) {
+  const DoneFlag done{done_count, done_flag, done_seq};
+  if (D <= 0 || D > 256 || S <= 0 || bh <= 0 || (done_flag != nullptr && stats != nullptr)) {
     return hipErrorInvalidValue;
   }
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
@@ -1975,7 +1952,7 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
   const bool dflt = splits == 0 && attentionF32DefaultSplits(bh, S, D) == kAttnF32Q16;
   if ((splits == kAttnF32Q16 || dflt) && attentionF32Q16Fits(D, k, v, q)) {
     const dim3 grid16((S + 15) / 16, bh);
-    const AttnSrcGlobal gsrc{q, k, v};
+    const AttnSrcGlobal gsrc{q, k, v, done};
 #define LC_ATTN_Q16(DQ_)                                                                                            \
   hipLaunchKernelGGL((attn_fwd_f32_q16_kernel<DQ_, 16, AttnSrcGlobal>), grid16, dim3(1024), 0, stream, gsrc, out,   \
                      stats, S, D, cz, scale, post_scale, post_bias, post_relu)
@@ -1994,7 +1971,7 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
   const int ks = attentionF32Splits(bh, S, D, splits == kAttnF32Q16 ? 0 : splits);
   const bool vec = dt <= 2 && D % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
                    reinterpret_cast<uintptr_t>(v) % 16 == 0;
-  const AttnSrcGlobal src{q, k, v};
+  const AttnSrcGlobal src{q, k, v, done};
 #define LC_ATTN_F32(DT_, KS_)                                                                                       \
   if (vec && (DT_) <= 2) {                                                                                          \
     hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, ((DT_) <= 2), AttnSrcGlobal>), grid, dim3(64 * (KS_)), 0,    \
@@ -2051,9 +2028,7 @@ hipError_t convAttentionF32(const float* x, const float* w, const float* bias, i
   AttnSrcConvRepeat src{x, w, bias, cin, h, wd, cout, kh, kw, sh, sw, ph, pw, oh, ow, static_cast<int>(n),
                         static_cast<int>(xs < big ? xs : big), static_cast<int>(ws < big ? ws : big),
                         static_cast<size_t>(S) * D};
-  src.done_count = done_count;
-  src.done_flag = done_flag;
-  src.done_seq = done_seq;
+  src.done = DoneFlag{done_count, done_flag, done_seq};
   const float scale = 1.0f / sqrtf(static_cast<float>(D));
   // D <= 64: the 16-query kernel (16 waves of 16-key tiles, 8 at D > 48 so
   // that the per-wave tiles fit next to the conv buffer).

@@ -163,6 +163,45 @@ __global__ __launch_bounds__(256) void repeat_fill_kernel(const float* __restric
   }
 }
 
+// dst_j[i] = src[j * n + i], j = 0, 1, 2: three tensors packed back to back
+// (in mapped host memory: each value crosses the bus once) into three
+// buffers.  VEC: n % 4 == 0 and every base 16-byte aligned.
+template <bool VEC>
+__global__ __launch_bounds__(256) void split3_copy_f32_kernel(const float* __restrict__ src, float* __restrict__ d0,
+                                                              float* __restrict__ d1, float* __restrict__ d2,
+                                                              size_t n) {
+  const size_t w = VEC ? n / 4 : n;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < 3 * w;
+       i += static_cast<size_t>(gridDim.x) * 256) {
+    const size_t j = i / w;
+    const size_t r = i - j * w;
+    float* d = j == 0 ? d0 : j == 1 ? d1 : d2;
+    if (VEC) {
+      reinterpret_cast<float4*>(d)[r] = reinterpret_cast<const float4*>(src)[i];
+    } else {
+      d[r] = src[i];
+    }
+  }
+}
+
+// dst[i] = src[i] for i < n into the device alias of pinned host memory, then
+// the launch's completion flag.  VEC: n % 4 == 0 and both bases 16-byte
+// aligned.
+template <bool VEC>
+__global__ __launch_bounds__(256) void copy_out_flag_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                            size_t n, DoneFlag done) {
+  const size_t w = VEC ? n / 4 : n;
+  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < w;
+       i += static_cast<size_t>(gridDim.x) * 256) {
+    if (VEC) {
+      reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(src)[i];
+    } else {
+      dst[i] = src[i];
+    }
+  }
+  done.finish_all_writers();
+}
+
 // out = a (op) b elementwise: 0 add, 1 sub, 2 div, 3 relu(a), 4 relu(a + b)
 // (and a + b to `sum` when it is not null).
 __global__ __launch_bounds__(256) void elementwise_f32_kernel(int op, const float* a, const float* b, float* out,
@@ -291,6 +330,38 @@ hipError_t repeatFillF32(const float* src, size_t n, float* dst, size_t total, h
     return hipErrorInvalidValue;
   }
   hipLaunchKernelGGL(repeat_fill_kernel, dim3(grid_for(total)), dim3(256), 0, stream, src, n, dst, total);
+  return hipGetLastError();
+}
+
+hipError_t split3CopyF32(const float* src, float* d0, float* d1, float* d2, size_t n, hipStream_t stream) {
+  if (n == 0) {
+    return hipSuccess;
+  }
+  const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(d0) |
+                                  reinterpret_cast<uintptr_t>(d1) | reinterpret_cast<uintptr_t>(d2)) % 16 == 0;
+  const size_t items = 3 * (vec ? n / 4 : n);
+  if (vec) {
+    hipLaunchKernelGGL(split3_copy_f32_kernel<true>, dim3(grid_for(items)), dim3(256), 0, stream, src, d0, d1, d2, n);
+  } else {
+    hipLaunchKernelGGL(split3_copy_f32_kernel<false>, dim3(grid_for(items)), dim3(256), 0, stream, src, d0, d1, d2, n);
+  }
+  return hipGetLastError();
+}
+
+hipError_t copyOutFlagF32(const float* src, float* dst, size_t n, unsigned* done_count, unsigned* done_flag,
+                          unsigned done_seq, hipStream_t stream) {
+  if (n == 0 || done_count == nullptr || done_flag == nullptr) {
+    return hipErrorInvalidValue;
+  }
+  const DoneFlag done{done_count, done_flag, done_seq};
+  const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 == 0;
+  const size_t items = vec ? n / 4 : n;
+  const int grid = grid_for(items) < 256 ? grid_for(items) : 256;
+  if (vec) {
+    hipLaunchKernelGGL(copy_out_flag_kernel<true>, dim3(grid), dim3(256), 0, stream, src, dst, n, done);
+  } else {
+    hipLaunchKernelGGL(copy_out_flag_kernel<false>, dim3(grid), dim3(256), 0, stream, src, dst, n, done);
+  }
   return hipGetLastError();
 }
 

@@ -247,4 +247,50 @@ __device__ __forceinline__ int acc_row(int i, int lane) {
   return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
 }
 
+// Optional completion flag of a synchronous small call: `flag` is a
+// host-mapped word the host spins on, `count` a device counter that starts at
+// zero.  Each workgroup makes its output visible to the host (system-scope
+// release) before thread 0 counts it with an acquire-release add at device
+// scope, so the last workgroup's count follows every other workgroup's
+// release; the last one zeroes the counter for the next launch and publishes
+// `seq` with a system-scope release store.
+struct DoneFlag {
+  unsigned* count = nullptr;
+  unsigned* flag = nullptr;
+  unsigned seq = 0;
+  // With a flag, the attention kernels let wave 0 store the workgroup's whole
+  // output, so one wave's release covers it.
+  __device__ bool single_writer() const { return flag != nullptr; }
+  // Every thread, after wave 0 stored the workgroup's whole output.
+  __device__ void finish() const {
+    if (flag == nullptr || threadIdx.x >= 64) {
+      return;
+    }
+    __threadfence_system();
+    if (threadIdx.x == 0) {
+      count_and_publish();
+    }
+  }
+  // Every thread, after storing its own share of the output: each wave
+  // releases its stores, then the barrier orders them before the count.
+  __device__ void finish_all_writers() const {
+    if (flag == nullptr) {
+      return;
+    }
+    __threadfence_system();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      count_and_publish();
+    }
+  }
+  __device__ void count_and_publish() const {
+    const unsigned total = gridDim.x * gridDim.y * gridDim.z;
+    if (__hip_atomic_fetch_add(count, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == total - 1) {
+      __hip_atomic_store(count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __threadfence_system();
+      __hip_atomic_store(flag, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+};
+
 }  // namespace lchip::k

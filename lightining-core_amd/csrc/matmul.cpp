@@ -294,6 +294,71 @@ Status settleVariant(HipContext* ctx, MatMulResident& r) {
   return Status::kSuccess;
 }
 
+// Small fp32 calls that upload both operands and download the product (the
+// plain matmul2d call) spend most of their time in per-copy overhead: two
+// pageable uploads and a pageable download at ~10 us each, and the stream
+// sync.  Here A and B are packed into pinned staging and the padding kernels
+// read them through its device alias (each value crosses the bus once); after
+// the GEMM one kernel copies C into the staging and raises the host-mapped
+// completion flag, which the call waits for instead of a stream sync.
+constexpr std::size_t kQuickMatMulElems = std::size_t{1} << 18;  // per operand and the product
+
+bool quickMatMulEnabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("CJ_HIP_MATMUL_QUICK");
+    return v == nullptr || std::string(v) != "0";
+  }();
+  return on;
+}
+
+Status matmulQuick(HipContext* ctx, MatMulResident& r, const float* a, const float* b, float* out) {
+  const std::size_t na = r.m * r.k, nb = r.k * r.n, nc = r.m * r.n;
+  const std::size_t b_at = roundUp(na, 64);  // 256-byte aligned parts
+  const std::size_t c_at = roundUp(b_at + nb, 64);
+  const std::size_t mp = roundUp(r.m, kern::kF32GemmBM);
+  const std::size_t kp = roundUp(r.k, kern::kF32GemmBK);
+  const std::size_t np = roundUp(r.n, kern::kF32GemmBN);
+  LC_TRY(ctx->pinned.ensure((c_at + nc) * sizeof(float)));
+  LC_TRY(r.a.ensure(mp * kp * sizeof(float)));
+  LC_TRY(r.b.ensure(kp * np * sizeof(float)));
+  LC_TRY(r.c.ensure(nc * sizeof(float)));
+  float* stage = static_cast<float*>(ctx->pinned.get());
+  float* dev = static_cast<float*>(ctx->pinned.device());
+  std::memcpy(stage, a, na * sizeof(float));
+  std::memcpy(stage + b_at, b, nb * sizeof(float));
+  hipError_t e = kern::padCopyF32(dev, r.a.as<float>(), static_cast<int>(r.m), static_cast<int>(r.k), r.k,
+                                  static_cast<int>(mp), static_cast<int>(kp), ctx->stream);
+  if (e == hipSuccess) {
+    e = kern::padCopyF32(dev + b_at, r.b.as<float>(), static_cast<int>(r.k), static_cast<int>(r.n), r.n,
+                         static_cast<int>(kp), static_cast<int>(np), ctx->stream);
+  }
+  if (e != hipSuccess) {
+    return failHip(e, "matmul upload padding");
+  }
+  r.has_a = r.has_b = true;
+  if (!r.tuned) {
+    LC_TRY(settleVariant(ctx, r));
+    r.tuned = true;
+  }
+  unsigned* flag_dev = nullptr;
+  unsigned* count_dev = nullptr;
+  unsigned seq = 0;
+  LC_TRY(prepareDoneFlag(ctx, &flag_dev, &count_dev, &seq));
+  traceOpDispatch(TraceOp::kMatMul, Device::kHIP, Device::kHIP, false, r.m * r.k * r.n);
+  e = launchGemm(ctx, r, r.variant);
+  if (e != hipSuccess) {
+    return failHip(e, "matmul kernel launch");
+  }
+  r.has_c = true;
+  e = kern::copyOutFlagF32(r.c.as<float>(), dev + c_at, nc, count_dev, flag_dev, seq, ctx->stream);
+  if (e != hipSuccess) {
+    return failHip(e, "matmul output copy");
+  }
+  LC_TRY(waitDoneFlag(ctx, seq));
+  std::memcpy(out, stage + c_at, nc * sizeof(float));
+  return Status::kSuccess;
+}
+
 }  // namespace
 
 Status matmulResident(HipContext* ctx, MatMulResident& r, std::size_t m, std::size_t k, std::size_t n,
@@ -320,6 +385,10 @@ Status matmulResident(HipContext* ctx, MatMulResident& r, std::size_t m, std::si
   }
   if ((!policy.upload_a && !r.has_a) || (!policy.upload_b && !r.has_b)) {
     return fail(Status::kInvalidValue, "matmul: no resident input for an operand the policy does not upload");
+  }
+  if (!isHalf(dtype) && repeat == 1 && policy.upload_a && policy.upload_b && policy.download_out &&
+      std::max({m * k, k * n, m * n}) <= kQuickMatMulElems && quickMatMulEnabled()) {
+    return matmulQuick(ctx, r, a, b, out);
   }
   if (policy.upload_a) {
     LC_TRY(uploadA(ctx, r, a));

@@ -115,6 +115,43 @@ def test_session_upload_once(lc, oracle):
         fresh.forward_with_policy(q, k, v, lc.AttentionIoPolicy(upload_q=False))
 
 
+def test_plain_calls_in_a_row_and_resident_reuse(lc, oracle):
+    """Plain calls (every input uploaded, output downloaded) of one head up to
+    65536 values per tensor stage through pinned memory and wait on a
+    completion flag; a run of them with changing shapes, causal and
+    postprocess settings, interleaved with the fused conv -> attention call
+    (which shares the staging and the flag), each sees its own result, and
+    the inputs a plain session call uploads stay resident for later calls."""
+    shapes = [(64, 32), (256, 64), (17, 5), (128, 256), (1, 8), (64, 32), (256, 256), (300, 200)]
+    x = synth.normal((1, 3, 8, 8), stream=330)
+    w = synth.normal((16, 3, 3, 3), stream=331)
+    for i, (s, d) in enumerate(shapes * 2):
+        q, k, v = (synth.normal((s, d), stream=340 + 3 * i + j) for j in range(3))
+        causal = i % 3 == 1
+        if i % 4 == 2:
+            pol = lc.AttentionIoPolicy(output_scale=0.5, output_bias=-0.1, output_relu=True)
+            got = lc.attention_forward_with_policy(q, k, v, s, d, causal, policy=pol).reshape(s, d)
+            exp = np.maximum(oracle.attention(q, k, v, causal) * 0.5 - 0.1, 0)
+        else:
+            got = lc.attention2d(q, k, v, causal)
+            exp = oracle.attention(q, k, v, causal)
+        assert_parity(exp, got, "f32", f"call {i}: S={s} D={d} causal={causal}")
+        if i % 5 == 4:
+            ca = lc.api.conv_attention_torchstrong_nchw(x, w, None, 48, 48, 1, 1, 1, 1)
+            ref = oracle.conv_attention(x, w, None, 48, 48, (1, 1), (1, 1))
+            assert_parity(ref.ravel(), np.asarray(ca).ravel(), "f32", f"conv {i}")
+    s, d = 256, 64
+    q, k, v = (synth.normal((s, d), stream=390 + j) for j in range(3))
+    sess = lc.AttentionSession(s, d, causal=True)
+    first = sess.forward_with_policy(q, k, v, lc.AttentionIoPolicy())
+    junk = np.full((s, d), np.nan, np.float32)
+    again = sess.forward_with_policy(junk, junk, junk, lc.AttentionIoPolicy(upload_q=False, upload_k=False,
+                                                                            upload_v=False))
+    exp = oracle.attention(q, k, v, True)
+    assert_parity(exp, first.reshape(s, d), "f32", "plain session call")
+    assert_parity(exp, again.reshape(s, d), "f32", "resident reuse after a plain call")
+
+
 def test_attention_trace(lc):
     lc.runtime_trace_clear()
     lc.runtime_trace_enable(True)

@@ -198,6 +198,34 @@ def test_policy_null_pointers_use_resident(lc, oracle):
         lc.matmul_with_policy(None, b, m, k, n, policy=lc.MatMulIoPolicy())
 
 
+def test_plain_calls_in_a_row_and_resident_reuse(lc, oracle):
+    """Plain fp32 calls (both operands uploaded, product downloaded) with at
+    most 2^18 values per operand and product stage through pinned memory and
+    wait on a completion flag raised by the kernel that copies the product
+    out.  A run of them with changing shapes (across the size cap), mixed with
+    plain attention calls that share the staging and the flag, each sees its
+    own result, and the operands a plain call uploads stay resident."""
+    shapes = [(1, 1, 1), (4, 7, 5), (64, 64, 64), (511, 512, 513), (512, 512, 512), (513, 512, 512),
+              (3, 1000, 2), (200, 33, 1300)]
+    for i, (m, k, n) in enumerate(shapes * 2):
+        a = synth.uniform((m, k), stream=500 + 2 * i)
+        b = synth.uniform((k, n), stream=501 + 2 * i)
+        got = lc.matmul2d(a, b)
+        assert_parity(oracle.matmul(a, b), got, "f32", f"call {i}: {m}x{k}x{n}")
+        if i % 3 == 2:
+            q, kk, v = (synth.normal((64, 32), stream=600 + 3 * i + j) for j in range(3))
+            assert_parity(oracle.attention(q, kk, v), lc.attention2d(q, kk, v), "f32", f"attention {i}")
+    m, k, n = 48, 40, 36
+    a = synth.uniform((m, k), stream=590)
+    b = synth.uniform((k, n), stream=591)
+    first = lc.matmul_with_policy(a, b, m, k, n, policy=lc.MatMulIoPolicy()).reshape(m, n)
+    run = lc.MatMulIoPolicy(upload_a=False, upload_b=False, download_out=True, synchronize=True)
+    again = lc.matmul_with_policy(None, None, m, k, n, policy=run).reshape(m, n)
+    exp = oracle.matmul(a, b)
+    assert_parity(exp, first, "f32", "plain policy call")
+    assert_parity(exp, again, "f32", "resident reuse after a plain call")
+
+
 def test_trace_records_hip_dispatch(lc):
     lc.runtime_trace_clear()
     lc.runtime_trace_enable(True)
