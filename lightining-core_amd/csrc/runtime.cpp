@@ -301,13 +301,19 @@ Status prepareDoneFlag(HipContext* ctx, unsigned** flag_dev, unsigned** count_de
 }
 
 Status waitDoneFlag(HipContext* ctx, unsigned seq) {
+  // Spin budget: 200 ms, or CJ_HIP_DONE_WAIT_US (read once; 0 takes the
+  // stream-sync path below at once).
+  static const long long budget_us = [] {
+    const char* v = std::getenv("CJ_HIP_DONE_WAIT_US");
+    return v != nullptr ? std::atoll(v) : 200000LL;
+  }();
   const unsigned* word = static_cast<const unsigned*>(ctx->done_flag.get());
   const auto t0 = std::chrono::steady_clock::now();
   for (;;) {
     if (__atomic_load_n(word, __ATOMIC_ACQUIRE) == seq) {
       return afterSync(ctx);
     }
-    if (std::chrono::steady_clock::now() - t0 > std::chrono::milliseconds(200)) {
+    if (std::chrono::steady_clock::now() - t0 >= std::chrono::microseconds(budget_us)) {
       break;
     }
   }

@@ -17,10 +17,17 @@
   src/ops/matmul_metal.mm:27, :1864-1878; attention 64,
   src/attention_metal.mm:26, :1448-1462): the capped call synchronises the
   stream and records a device_synchronize trace event, and the results of
-  the enqueued launches match the oracle.
+  the enqueued launches match the oracle;
+* the completion-flag wait of plain calls with host arrays (attention2d,
+  matmul2d, the fused conv -> attention call): with its spin budget forced to
+  0 from the host (CJ_HIP_DONE_WAIT_US, read once, so in a child process)
+  every call takes the stream-sync path, and calls in a row stay right.
 """
 import ctypes
 import os
+import subprocess
+import sys
+import textwrap
 import threading
 
 import numpy as np
@@ -265,3 +272,37 @@ def test_enqueue_only_launches_are_capped(lc, oracle):
 
 def lc_status_name(code):
     return N.load().lcGetErrorString(code).decode()
+
+
+def test_done_flag_wait_falls_back_to_stream_sync(lc):
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    env = {k: v for k, v in os.environ.items() if not k.startswith("CJ_")}
+    env["CJ_HIP_DONE_WAIT_US"] = "0"
+    env["PYTHONPATH"] = os.pathsep.join([os.path.join(root, "lightining-core_amd"), os.path.dirname(__file__),
+                                         env.get("PYTHONPATH", "")])
+    code = """
+        import numpy as np
+        import lightning_core as lc
+        import oracle_lib
+        from lightning_core import synth
+        from gpu_util import assert_parity
+        orc = oracle_lib.load()
+        x = synth.normal((1, 3, 8, 8), stream=700)
+        w = synth.normal((16, 3, 3, 3), std=0.3, stream=701)
+        conv_ref = orc.conv_attention(x, w, None, 48, 48, (1, 1), (1, 1)).ravel()
+        for i in range(6):
+            s, d = ((64, 32), (256, 64), (33, 200))[i % 3]
+            q, k, v = (synth.normal((s, d), stream=710 + 3 * i + j) for j in range(3))
+            causal = i % 2 == 1
+            assert_parity(orc.attention(q, k, v, causal), lc.attention2d(q, k, v, causal), "f32", f"attention {i}")
+            m, kk, n = ((64, 64, 64), (100, 77, 130), (1, 5, 300))[i % 3]
+            a, b = synth.uniform((m, kk), stream=740 + 2 * i), synth.uniform((kk, n), stream=741 + 2 * i)
+            assert_parity(orc.matmul(a, b), lc.matmul2d(a, b), "f32", f"matmul {i}")
+            got = np.asarray(lc.api.conv_attention_torchstrong_nchw(x, w, None, 48, 48, 1, 1, 1, 1)).ravel()
+            assert_parity(conv_ref, got, "f32", f"conv attention {i}")
+        print("ok")
+    """
+    note("[case] plain calls with the completion-flag spin budget 0 (child process)")
+    r = subprocess.run([sys.executable, "-u", "-c", textwrap.dedent(code)], cwd=root, env=env, capture_output=True,
+                       text=True, timeout=110)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stdout[-3000:] + r.stderr[-3000:]
