@@ -12,7 +12,9 @@
 // this library a request that the HIP kernels cannot serve returns an error.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
+#include <string>
 #include <memory>
 #include <vector>
 
@@ -138,6 +140,21 @@ int pickSplits(const std::vector<int>& cands, const std::vector<float>& ms, int 
   return best;
 }
 
+// The fp32 forward's key splits: on unless CJ_HIP_ATTN_KEY_SPLIT=0 (read
+// once; without a workspace every call runs unsplit).
+bool keySplitEnabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("CJ_HIP_ATTN_KEY_SPLIT");
+    return v == nullptr || std::string(v) != "0";
+  }();
+  return on;
+}
+
+// The fp32 forward's key-split workspace, grown to at least `floats`.
+Status ensureSplitWs(AttnResident& res, std::size_t floats) {
+  return floats > 0 && keySplitEnabled() ? res.split_ws.ensure(floats * sizeof(float)) : Status::kSuccess;
+}
+
 // Split counts worth timing for one head: the valid ones (LDS limits) up to
 // the number of 32-key tiles.
 std::vector<int> splitCandidates(int S, int D) {
@@ -177,13 +194,19 @@ Status forwardSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, co
   int best = kern::attentionF32DefaultSplits(1, S, D);
   const std::vector<int> cands = splitCandidates(S, D);
   if (cands.size() > 1 && autotuneEnabled("CJ_ATTN_AUTOTUNE")) {
+    std::size_t ws = 0;
+    for (int ks : cands) {
+      ws = std::max(ws, kern::attentionF32WorkspaceFloats(1, S, D, ks));
+    }
+    LC_TRY(ensureSplitWs(res, ws));
     std::vector<float> ms;
     LC_TRY(timeCandidates(
         ctx, cands,
         [&](int ks) {
           return kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(), 1,
                                     S, D, sh.causal, policy.output_scale, policy.output_bias, policy.output_relu,
-                                    nullptr, ctx->stream, ks);
+                                    nullptr, ctx->stream, ks, nullptr, nullptr, 0, res.split_ws.as<float>(),
+                                    res.split_ws.size() / sizeof(float));
         },
         &ms));
     best = pickSplits(cands, ms, best);
@@ -278,14 +301,16 @@ Status attentionForwardQuick(HipContext* ctx, AttnResident& res, const AttnShape
   unsigned* flag_dev = nullptr;
   unsigned* count_dev = nullptr;
   unsigned seq = 0;
-  LC_TRY(prepareDoneFlag(ctx, &flag_dev, &count_dev, &seq));
   const int S = static_cast<int>(sh.seq_len);
   const int D = static_cast<int>(sh.head_dim);
+  LC_TRY(ensureSplitWs(res, kern::attentionF32WorkspaceFloats(1, S, D, splits)));
+  LC_TRY(prepareDoneFlag(ctx, &flag_dev, &count_dev, &seq));
   traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, sh.seq_len * sh.seq_len * sh.head_dim);
   const hipError_t e = kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(),
                                           static_cast<float*>(ctx->pinned.device()) + out_at, 1, S, D, sh.causal,
                                           policy.output_scale, policy.output_bias, policy.output_relu, nullptr,
-                                          ctx->stream, splits, count_dev, flag_dev, seq);
+                                          ctx->stream, splits, count_dev, flag_dev, seq, res.split_ws.as<float>(),
+                                          res.split_ws.size() / sizeof(float));
   if (e != hipSuccess) {
     return failHip(e, "attention kernel launch");
   }
@@ -352,13 +377,17 @@ Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnSh
   if (!half && bh == 1 && repeat > 0) {
     LC_TRY(forwardSplits(ctx, res, sh, policy, &splits));
   }
+  if (!half) {
+    LC_TRY(ensureSplitWs(res, kern::attentionF32WorkspaceFloats(bh, S, D, splits)));
+  }
   for (std::size_t r = 0; r < repeat; ++r) {
     traceOpDispatch(TraceOp::kAttentionForward, Device::kHIP, Device::kHIP, false, hint);
     hipError_t e;
     if (!half) {
       e = kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(), bh, S, D,
                              sh.causal, policy.output_scale, policy.output_bias, policy.output_relu, nullptr,
-                             ctx->stream, splits);
+                             ctx->stream, splits, nullptr, nullptr, 0, res.split_ws.as<float>(),
+                             res.split_ws.size() / sizeof(float));
     } else {
       e = kern::attentionHalf(res.q.as<uint16_t>(), res.k.as<uint16_t>(), res.v.as<uint16_t>(), res.out.as<float>(),
                               nullptr, static_cast<int>(sh.heads), bh, S, static_cast<int>(sh.sPad()), D, sh.causal,
@@ -436,8 +465,10 @@ Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShap
   const int D = static_cast<int>(sh.head_dim);
   // The step's forward has no postprocess (the reference applies it only in
   // attentionForwardWithPolicy, src/attention.cpp:41-60).
+  LC_TRY(ensureSplitWs(res, kern::attentionF32WorkspaceFloats(1, S, D, 0)));
   hipError_t e = kern::attentionF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(), 1,
-                                    S, D, sh.causal, 1.0f, 0.0f, 0, res.stats.as<float>(), ctx->stream);
+                                    S, D, sh.causal, 1.0f, 0.0f, 0, res.stats.as<float>(), ctx->stream, 0, nullptr,
+                                    nullptr, 0, res.split_ws.as<float>(), res.split_ws.size() / sizeof(float));
   if (e == hipSuccess && loss_out != nullptr) {
     e = kern::mseLossF32(res.out.as<float>(), res.target.as<float>(), n,
                          1.0f / static_cast<float>(sh.seq_len * sh.head_dim), res.loss.as<float>(), ctx->stream);

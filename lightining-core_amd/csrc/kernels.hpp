@@ -95,10 +95,17 @@ hipError_t postprocessF32(float* x, size_t n, float scale, float bias, int relu,
 // D <= 256.  Output postprocess relu?(o*post_scale + post_bias).  stats
 // (optional, [bh, S, 2]) receives each query's softmax max m and sum l in the
 // log2 domain (p = exp2((q.k)*scale*log2(e) - m) / l).
+// With split_ws (device, split_ws_floats of it), a call whose 32-query grid
+// would cover fewer than half the CUs divides the key tiles of each query
+// block among workgroups that write partial results there; a second kernel
+// merges them (attentionF32WorkspaceFloats: the floats such a call needs, 0
+// when it would not split).
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D,
                         bool causal, float post_scale, float post_bias, int post_relu, float* stats,
                         hipStream_t stream, int splits = 0, unsigned* done_count = nullptr,
-                        unsigned* done_flag = nullptr, unsigned done_seq = 0);
+                        unsigned* done_flag = nullptr, unsigned done_seq = 0, float* split_ws = nullptr,
+                        size_t split_ws_floats = 0);
+size_t attentionF32WorkspaceFloats(int bh, int S, int D, int splits);
 // The `splits` value that selects the 16-query fp32 forward kernel
 // (attn_fwd_f32_q16_kernel: 16 waves of 16-key tiles per 16 queries), for
 // problems too small to fill the GPU.  Needs D <= 64, D % 4 == 0 and 16-byte

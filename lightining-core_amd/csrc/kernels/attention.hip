@@ -283,7 +283,7 @@ template <int DT, int KS, bool VEC, typename Src>
 __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* __restrict__ out,
                                                                float* __restrict__ stats, int S, int D, int causal,
                                                                float scale, float post_scale, float post_bias,
-                                                               int post_relu) {
+                                                               int post_relu, int split_tiles, float* __restrict__ ws) {
   constexpr int DP = 32 * DT;
   // Q and K rows have stride DP + 4: 16-byte aligned (float4 reads), and a
   // 16-lane pass of one float4 per row touches 16 distinct bank groups.
@@ -298,13 +298,24 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
   float (*Ks)[QKS] = reinterpret_cast<float (*)[QKS]>(&kv[wave][0]);
   float (*Vs)[DP] = reinterpret_cast<float (*)[DP]>(&kv[wave][32 * QKS]);
   // Workgroup qb: query block qb; its waves take the 32-key tiles w + KS n.
-  // Heaviest (causal) blocks first.
+  // Heaviest (causal) blocks first.  Key split (split_tiles > 0): workgroup
+  // z = blockIdx.z takes only the tiles [z, z + 1) * split_tiles and writes
+  // its unnormalised partial (O, m, l) to ws for attn_split_combine_kernel:
+  // O [z][head][S][D], then (m, l) [z][head][S][2].
+  const bool split = split_tiles > 0;
   const int nqb = (S + 31) / 32;
   const int qb = nqb - 1 - static_cast<int>(blockIdx.x);
   const int q0 = qb * 32;
-  const int jfirst = wave * 32;
+  const int kbeg = split ? static_cast<int>(blockIdx.z) * split_tiles * 32 : 0;
+  const int jfirst = kbeg + wave * 32;
   const int jstep = 32 * KS;
   const size_t head = static_cast<size_t>(blockIdx.y) * S * D;
+  float* ml = nullptr;
+  if (split) {
+    out = ws + static_cast<size_t>(blockIdx.z) * gridDim.y * S * D;
+    ml = ws + static_cast<size_t>(gridDim.z) * gridDim.y * S * D +
+         (static_cast<size_t>(blockIdx.z) * gridDim.y + blockIdx.y) * S * 2;
+  }
   out += head;
   src.prologue(srcbuf, 64 * KS);
 
@@ -316,15 +327,22 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
   float m_run = kMaskValue;
   float l_run = 0.0f;
   const int qi = q0 + (lane & 31);
-  const int kend = causal ? min(S, q0 + 32) : S;
+  int kend = causal ? min(S, q0 + 32) : S;
+  if (split) {
+    kend = min(kend, kbeg + split_tiles * 32);
+  }
 
   // Only this wave touches its K / V tiles: wave-level ordering suffices
   // (LDS accesses of one wave complete in order).  VEC (D % 4 == 0, 16-byte
-  // aligned rows, DT <= 2): each lane holds CH float4 of the next tile's K
-  // and V in registers, loaded while the current tile is computed.
+  // aligned rows): tiles move as float4.  DT <= 2 (PREF): each lane holds CH
+  // float4 of the next tile's K and V in registers, loaded while the current
+  // tile is computed; wider tiles (FILL4) are loaded and stored in groups of
+  // four chunks at the top of each tile.
+  constexpr bool PREF = VEC && DT <= 2;
+  constexpr bool FILL4 = VEC && DT > 2;
   constexpr int CH = DP / 8;  // float4 chunks per lane per operand
-  float4 kr[VEC ? CH : 1];
-  float4 vr[VEC ? CH : 1];
+  float4 kr[PREF ? CH : 1];
+  float4 vr[PREF ? CH : 1];
   auto fetch = [&](int j0) {
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
@@ -333,7 +351,7 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
       const int cc = (idx - r * (DP / 4)) * 4;
       const bool ok = j0 + r < S && cc < D;
       const size_t off = static_cast<size_t>(j0 + r) * D + cc;
-      if constexpr (VEC) {
+      if constexpr (PREF) {
         kr[c] = ok ? *reinterpret_cast<const float4*>(src.k + head + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         vr[c] = ok ? *reinterpret_cast<const float4*>(src.v + head + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
       }
@@ -341,7 +359,7 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
   };
   // The first K / V tile's loads go out before the Q tile's, so their
   // latencies overlap.
-  if constexpr (VEC) {
+  if constexpr (PREF) {
     if (jfirst < kend) {
       fetch(jfirst);
     }
@@ -349,7 +367,7 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
   fill_rows<DP, 1, 0, 0>(src, srcbuf, &Qs[0][0], QKS, nullptr, 0, wave, KS, q0, S, D, head, lane);
   __syncthreads();
   for (int j0 = jfirst; j0 < kend; j0 += jstep) {
-    if constexpr (VEC) {
+    if constexpr (PREF) {
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
         const int idx = c * 64 + lane;
@@ -360,6 +378,29 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
       }
       if (j0 + jstep < kend) {
         fetch(j0 + jstep);
+      }
+    } else if constexpr (FILL4) {
+      for (int c0 = 0; c0 < CH; c0 += 4) {
+        float4 kx[4];
+        float4 vx[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int idx = (c0 + c) * 64 + lane;
+          const int r = idx / (DP / 4);
+          const int cc = (idx - r * (DP / 4)) * 4;
+          const bool ok = j0 + r < S && cc < D;
+          const size_t off = static_cast<size_t>(j0 + r) * D + cc;
+          kx[c] = ok ? *reinterpret_cast<const float4*>(src.k + head + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          vx[c] = ok ? *reinterpret_cast<const float4*>(src.v + head + off) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const int idx = (c0 + c) * 64 + lane;
+          const int r = idx / (DP / 4);
+          const int cc = (idx - r * (DP / 4)) * 4;
+          *reinterpret_cast<float4*>(&Ks[r][cc]) = kx[c];
+          *reinterpret_cast<float4*>(&Vs[r][cc]) = vx[c];
+        }
       }
     } else {
       fill_rows<DP, 2, 1, 2>(src, srcbuf, &Ks[0][0], QKS, &Vs[0][0], DP, 0, 1, j0, S, D, head, lane);
@@ -484,13 +525,17 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
       stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2] = m_all;
       stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2 + 1] = l_all;
     }
+    if (split && wave == 0 && lane < 32 && qi < S) {
+      ml[qi * 2] = m_all;
+      ml[qi * 2 + 1] = l_all;
+    }
     for (int d = 2 * wave + (lane >> 5); d < D; d += 2 * KS) {
       float acc = 0.0f;
 #pragma unroll
       for (int w = 0; w < KS; ++w) {
         acc += f[w] * kv[w][64 + ql * PS + d];
       }
-      tile[ql * TS + d] = post(acc * inv);
+      tile[ql * TS + d] = split ? acc : post(acc * inv);
     }
   } else {
     const float inv = 1.0f / l_run;
@@ -498,13 +543,17 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
       stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2] = m_run;
       stats[(static_cast<size_t>(blockIdx.y) * S + qi) * 2 + 1] = l_run;
     }
+    if (split && lane < 32 && qi < S) {
+      ml[qi * 2] = m_run;
+      ml[qi * 2 + 1] = l_run;
+    }
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int d = t * 32 + acc_row(i, lane);
         if (d < D) {
-          tile[ql * TS + d] = post(o[t][i] * inv);
+          tile[ql * TS + d] = split ? o[t][i] : post(o[t][i] * inv);
         }
       }
     }
@@ -527,6 +576,51 @@ __global__ __launch_bounds__(64 * KS) void attn_fwd_f32_kernel(Src src, float* _
     }
   }
   src.finish();
+}
+
+// Merges attn_fwd_f32_kernel's key splits: per query row, M = max_z m_z,
+// L = sum_z l_z exp2(m_z - M) and out = post(sum_z O_z exp2(m_z - M) / L),
+// splits summed in z order; stats (optional) receive (M, L).  One wave per
+// row, four rows per workgroup; every thread reaches the completion flag.
+__global__ __launch_bounds__(256) void attn_split_combine_kernel(const float* __restrict__ ws, float* __restrict__ out,
+                                                                 float* __restrict__ stats, int rows, int D,
+                                                                 int nsplit, float post_scale, float post_bias,
+                                                                 int post_relu, DoneFlag done) {
+  const int row = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row < rows) {
+    const float* ml = ws + static_cast<size_t>(nsplit) * rows * D;
+    float m_all = kMaskValue;
+    for (int z = 0; z < nsplit; ++z) {
+      m_all = fmaxf(m_all, ml[(static_cast<size_t>(z) * rows + row) * 2]);
+    }
+    float l_all = 0.0f;
+    for (int z = 0; z < nsplit; ++z) {
+      const float* p = ml + (static_cast<size_t>(z) * rows + row) * 2;
+      l_all += p[1] * exp2f(p[0] - m_all);
+    }
+    const float inv = 1.0f / l_all;
+    for (int d = lane; d < D; d += 64) {
+      float acc = 0.0f;
+      for (int z = 0; z < nsplit; ++z) {
+        acc += ws[(static_cast<size_t>(z) * rows + row) * D + d] *
+               exp2f(ml[(static_cast<size_t>(z) * rows + row) * 2] - m_all);
+      }
+      float val = acc * inv;
+      if (post_scale != 1.0f || post_bias != 0.0f || post_relu) {
+        val = val * post_scale + post_bias;
+        if (post_relu && val < 0.0f) {
+          val = 0.0f;
+        }
+      }
+      out[static_cast<size_t>(row) * D + d] = val;
+    }
+    if (stats != nullptr && lane == 0) {
+      stats[static_cast<size_t>(row) * 2] = m_all;
+      stats[static_cast<size_t>(row) * 2 + 1] = l_all;
+    }
+  }
+  done.finish_all_writers();
 }
 
 // ---------------------------------------------------------------------------
@@ -1936,9 +2030,51 @@ int attentionF32Splits(int bh, int S, int D, int requested) {
   return ks;
 }
 
+namespace {
+
+// 32-key tiles per key split of the 32-query kernel, 0 for none: while its
+// grid (query blocks x heads) covers fewer than half the CUs, the key tiles
+// of a block are divided among up to 16 workgroups (a power of two, grid at
+// most 256 workgroups, every wave still with at least one tile).
+int keySplitTiles(int bh, int S, int ks) {
+  const int nqb = (S + 31) / 32;
+  const long long base = static_cast<long long>(nqb) * bh;
+  if (base >= 128) {
+    return 0;
+  }
+  int n = 1;
+  while (n < 16 && base * (2 * n) <= 256 && 2LL * n * ks <= nqb) {
+    n *= 2;
+  }
+  return n > 1 ? (nqb + n - 1) / n : 0;
+}
+
+// The q16 kernel would serve this call (its pointer-alignment condition aside).
+bool q16Serves(int bh, int S, int D, int splits) {
+  return (splits == kAttnF32Q16 || (splits == 0 && attentionF32DefaultSplits(bh, S, D) == kAttnF32Q16)) &&
+         D <= 64 && D % 4 == 0;
+}
+
+}  // namespace
+
+size_t attentionF32WorkspaceFloats(int bh, int S, int D, int splits) {
+  if (D <= 0 || D > 256 || S <= 0 || bh <= 0 || q16Serves(bh, S, D, splits)) {
+    return 0;
+  }
+  const int ks = attentionF32Splits(bh, S, D, splits == kAttnF32Q16 ? 0 : splits);
+  const int tiles = keySplitTiles(bh, S, ks);
+  if (tiles == 0) {
+    return 0;
+  }
+  const int nqb = (S + 31) / 32;
+  const size_t nsplit = static_cast<size_t>((nqb + tiles - 1) / tiles);
+  return nsplit * static_cast<size_t>(bh) * S * (D + 2);
+}
+
 hipError_t attentionF32(const float* q, const float* k, const float* v, float* out, int bh, int S, int D, bool causal,
                         float post_scale, float post_bias, int post_relu, float* stats, hipStream_t stream,
-                        int splits, unsigned* done_count, unsigned* done_flag, unsigned done_seq) {
+                        int splits, unsigned* done_count, unsigned* done_flag, unsigned done_seq, float* split_ws,
+                        size_t split_ws_floats) {
   const DoneFlag done{done_count, done_flag, done_seq};
   if (D <= 0 || D > 256 || S <= 0 || bh <= 0 || (done_flag != nullptr && stats != nullptr)) {
     return hipErrorInvalidValue;
@@ -1966,19 +2102,30 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
     return hipGetLastError();
   }
   const int nqb = (S + 31) / 32;
-  const dim3 grid(nqb, bh);
   const int dt = (D + 31) / 32;
   const int ks = attentionF32Splits(bh, S, D, splits == kAttnF32Q16 ? 0 : splits);
-  const bool vec = dt <= 2 && D % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
-                   reinterpret_cast<uintptr_t>(v) % 16 == 0;
-  const AttnSrcGlobal src{q, k, v, done};
+  // Key split when the caller's workspace holds the partials; the combine
+  // kernel then writes out / stats and raises the completion flag.
+  int split_tiles = keySplitTiles(bh, S, ks);
+  const int nsplit = split_tiles > 0 ? (nqb + split_tiles - 1) / split_tiles : 1;
+  const size_t need = static_cast<size_t>(nsplit) * bh * S * (D + 2);
+  if (split_tiles > 0 && (split_ws == nullptr || split_ws_floats < need)) {
+    split_tiles = 0;
+  }
+  const bool split = split_tiles > 0;
+  const dim3 grid(nqb, bh, split ? nsplit : 1);
+  const bool vec = D % 4 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0;
+  const AttnSrcGlobal src{q, k, v, split ? DoneFlag{} : done};
+  float* const stats_main = split ? nullptr : stats;
 #define LC_ATTN_F32(DT_, KS_)                                                                                       \
-  if (vec && (DT_) <= 2) {                                                                                          \
-    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, ((DT_) <= 2), AttnSrcGlobal>), grid, dim3(64 * (KS_)), 0,    \
-                       stream, src, out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);    \
+  if (vec) {                                                                                                        \
+    hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, true, AttnSrcGlobal>), grid, dim3(64 * (KS_)), 0,            \
+                       stream, src, out, stats_main, S, D, cz, scale, post_scale, post_bias, post_relu,           \
+                       split_tiles, split_ws);                                                                      \
   } else {                                                                                                          \
     hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false, AttnSrcGlobal>), grid, dim3(64 * (KS_)), 0, stream,   \
-                       src, out, stats, S, D, cz, scale, post_scale, post_bias, post_relu);            \
+                       src, out, stats_main, S, D, cz, scale, post_scale, post_bias, post_relu, split_tiles,      \
+                       split_ws);                                                                                   \
   }
 #define LC_ATTN_F32_KS(DT_)                                                                                         \
   switch (ks) {                                                                                                     \
@@ -1999,6 +2146,11 @@ hipError_t attentionF32(const float* q, const float* k, const float* v, float* o
   }
 #undef LC_ATTN_F32_KS
 #undef LC_ATTN_F32
+  if (split) {
+    const int rows = bh * S;
+    hipLaunchKernelGGL(attn_split_combine_kernel, dim3((rows + 3) / 4), dim3(256), 0, stream, split_ws, out, stats,
+                       rows, D, nsplit, post_scale, post_bias, post_relu, done);
+  }
   return hipGetLastError();
 }
 
@@ -2056,7 +2208,7 @@ hipError_t convAttentionF32(const float* x, const float* w, const float* bias, i
   }
 #define LC_CA_F32(DT_, KS_)                                                                                         \
   hipLaunchKernelGGL((attn_fwd_f32_kernel<DT_, KS_, false, AttnSrcConvRepeat>), grid, dim3(64 * (KS_)), 0, stream, \
-                     src, out, nullptr, S, D, 0, scale, 1.0f, 0.0f, 0)
+                     src, out, nullptr, S, D, 0, scale, 1.0f, 0.0f, 0, 0, nullptr)
 #define LC_CA_F32_KS(DT_)                                                                                           \
   switch (ks) {                                                                                                     \
     case 4: LC_CA_F32(DT_, (DT_ <= 2 ? 4 : 1)); break;                                                              \

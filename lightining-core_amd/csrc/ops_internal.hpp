@@ -33,6 +33,7 @@ struct AttnResident {
   DeviceBuffer q, k, v, out, stage;
   DeviceBuffer target, stats, loss;
   DeviceBuffer v_scratch;  // the train step's dV autotune runs on a copy of V
+  DeviceBuffer split_ws;   // partials of the fp32 forward's key splits
   bool has_q = false, has_k = false, has_v = false, has_out = false, has_target = false;
 };
 

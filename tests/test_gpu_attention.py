@@ -57,6 +57,27 @@ def test_attention_f32(lc, oracle, s, d, causal):
     assert_parity(oracle.attention(q, k, v, causal), got, "f32", f"f32 S={s} D={d} causal={causal}")
 
 
+@pytest.mark.parametrize("s,d,causal", [(2048, 64, True), (1024, 128, False), (700, 200, True), (256, 256, False),
+                                        (33, 256, True), (1100, 36, False)])
+def test_attention_f32_key_split(lc, oracle, s, d, causal):
+    # Grids of fewer than 128 query blocks divide each block's keys among up
+    # to 16 workgroups (a causal block's later splits can be empty: S=33);
+    # a second kernel merges the partials in split order, so repeated calls
+    # give the same bits.
+    q, k, v = (synth.normal((s, d), stream=800 + i) for i in range(3))
+    got = lc.attention2d(q, k, v, causal)
+    assert_parity(oracle.attention(q, k, v, causal), got, "f32", f"f32 key split S={s} D={d} causal={causal}")
+    np.testing.assert_array_equal(lc.attention2d(q, k, v, causal), got)
+
+
+def test_attention_f32_batched_key_split(lc, oracle):
+    b, h, s, d = 1, 3, 300, 128
+    q, k, v = (synth.normal((b, h, s, d), stream=820 + i) for i in range(3))
+    got = lc.attention_batched(q, k, v, True, "f32")
+    for hi in range(h):
+        assert_parity(oracle.attention(q[0, hi], k[0, hi], v[0, hi], True), got[0, hi], "f32", f"f32 batched head {hi}")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f16"])
 @pytest.mark.parametrize("b,h,s,d,causal", [(1, 2, 70, 64, True), (2, 3, 196, 64, False), (1, 2, 33, 128, True),
                                             (1, 1, 300, 128, False), (2, 2, 128, 64, True)])
