@@ -241,13 +241,19 @@ Status trainSplits(HipContext* ctx, AttnResident& res, const AttnShape& sh, cons
     const std::size_t bytes = sh.elems() * sizeof(float);
     LC_TRY(res.v_scratch.ensure(bytes));
     LC_HIP_TRY(hipMemcpyAsync(res.v_scratch.get(), res.v.get(), bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    std::size_t ws = 0;
+    for (int ks : cands) {
+      ws = std::max(ws, kern::attentionDvWorkspaceFloats(1, S, D, ks));
+    }
+    LC_TRY(ensureSplitWs(res, ws));
     std::vector<float> ms;
     LC_TRY(timeCandidates(
         ctx, cands,
         [&](int ks) {
           return kern::attentionDvUpdateF32(res.q.as<float>(), res.k.as<float>(), res.v_scratch.as<float>(),
                                             res.out.as<float>(), res.target.as<float>(), res.stats.as<float>(), 1, S,
-                                            D, sh.causal, lr, ctx->stream, ks);
+                                            D, sh.causal, lr, ctx->stream, ks, res.split_ws.as<float>(),
+                                            res.split_ws.size() / sizeof(float));
         },
         &ms));
     best = pickSplits(cands, ms, best);
@@ -460,7 +466,8 @@ Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShap
   }
   LC_TRY(res.out.ensure(bytes));
   LC_TRY(res.stats.ensure(sh.seq_len * 2 * sizeof(float)));
-  LC_TRY(res.loss.ensure(sizeof(float)));
+  // loss, the reduction's partials, its counter (zero at allocation, left at zero by every launch)
+  LC_TRY(res.loss.ensure((2 + kern::kMseLossMaxBlocks) * sizeof(float), true));
   const int S = static_cast<int>(sh.seq_len);
   const int D = static_cast<int>(sh.head_dim);
   // The step's forward has no postprocess (the reference applies it only in
@@ -471,16 +478,19 @@ Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShap
                                     nullptr, 0, res.split_ws.as<float>(), res.split_ws.size() / sizeof(float));
   if (e == hipSuccess && loss_out != nullptr) {
     e = kern::mseLossF32(res.out.as<float>(), res.target.as<float>(), n,
-                         1.0f / static_cast<float>(sh.seq_len * sh.head_dim), res.loss.as<float>(), ctx->stream);
+                         1.0f / static_cast<float>(sh.seq_len * sh.head_dim), res.loss.as<float>(), ctx->stream,
+                         res.loss.as<float>() + 1,
+                         reinterpret_cast<unsigned*>(res.loss.as<float>() + 1 + kern::kMseLossMaxBlocks));
   }
   if (e != hipSuccess) {
     return failHip(e, "attention train step launch");
   }
   int splits = 0;
   LC_TRY(trainSplits(ctx, res, sh, policy, loss_out != nullptr, learning_rate, &splits));
+  LC_TRY(ensureSplitWs(res, kern::attentionDvWorkspaceFloats(1, S, D, splits)));
   e = kern::attentionDvUpdateF32(res.q.as<float>(), res.k.as<float>(), res.v.as<float>(), res.out.as<float>(),
                                  res.target.as<float>(), res.stats.as<float>(), 1, S, D, sh.causal, learning_rate,
-                                 ctx->stream, splits);
+                                 ctx->stream, splits, res.split_ws.as<float>(), res.split_ws.size() / sizeof(float));
   if (e != hipSuccess) {
     return failHip(e, "attention train step launch");
   }

@@ -137,11 +137,23 @@ bool convAttentionStagesInputs(int batch, int cin, int h, int wd, int cout, int 
                                int pw);
 // Train step backward: v -= lr * P^T . (2 (out - target) / (S*D)) per head,
 // P recomputed from q, k and the forward's stats.
+// With split_ws, small grids divide each key block's query tiles among
+// workgroups writing partial dV there, summed and applied by a second kernel
+// (attentionDvWorkspaceFloats: the floats such a call needs, 0 when it would
+// not split).
 hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const float* out, const float* target,
                                 const float* stats, int bh, int S, int D, bool causal, float lr,
-                                hipStream_t stream, int splits = 0);
-// *loss = norm * sum_i (out_i - target_i)^2 (one workgroup, fixed order).
-hipError_t mseLossF32(const float* out, const float* target, size_t n, float norm, float* loss, hipStream_t stream);
+                                hipStream_t stream, int splits = 0, float* split_ws = nullptr,
+                                size_t split_ws_floats = 0);
+size_t attentionDvWorkspaceFloats(int bh, int S, int D, int splits);
+// *loss = norm * sum_i (out_i - target_i)^2 in a fixed order: contiguous
+// chunks of 16384 elements per workgroup (at most kMseLossMaxBlocks), their
+// partials added in chunk order by the last workgroup to finish.  partials
+// holds kMseLossMaxBlocks floats and counter starts (and is left) at zero;
+// without them one workgroup sums everything.
+constexpr int kMseLossMaxBlocks = 64;
+hipError_t mseLossF32(const float* out, const float* target, size_t n, float norm, float* loss, hipStream_t stream,
+                      float* partials = nullptr, unsigned* counter = nullptr);
 
 // ---- 16-bit ------------------------------------------------------------------
 // dst[b][r][c] = half(src[b][r][c]) for r < rows, c < cols; 0 up to

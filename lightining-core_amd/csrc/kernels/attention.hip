@@ -892,7 +892,8 @@ __global__ __launch_bounds__(64 * KS) void attn_dv_f32_kernel(const float* __res
                                                               const float* __restrict__ out,
                                                               const float* __restrict__ target,
                                                               const float* __restrict__ stats, int S, int D,
-                                                              int causal, float scale, float lr) {
+                                                              int causal, float scale, float lr, int split_qt,
+                                                              float* __restrict__ ws) {
   constexpr int DP = 32 * DT;
   constexpr int QO = 32 * (DP + 1) + 32 * DP;  // floats of one wave's Q + dO tile
   __shared__ float Ks[32][DP + 1];
@@ -926,8 +927,14 @@ __global__ __launch_bounds__(64 * KS) void attn_dv_f32_kernel(const float* __res
   const int key = j0 + (lane & 31);
   const int nqt = (S + 31) / 32;
   // Causal: query tile I meets key block J only when some query >= some key.
+  // Query split (split_qt > 0): workgroup z = blockIdx.z takes only the query
+  // tiles [z, z + 1) * split_qt and writes its partial dV [z][head][S][D] to
+  // ws (zeros when it meets none); attn_dv_split_combine_kernel sums the
+  // splits and updates V.
+  const int qlo = split_qt > 0 ? static_cast<int>(blockIdx.z) * split_qt : 0;
+  const int qhi = split_qt > 0 ? min(nqt, qlo + split_qt) : nqt;
   const bool vec = (D & 3) == 0;
-  for (int qt = (causal ? blockIdx.x : 0) + wave; qt < nqt; qt += KS) {
+  for (int qt = max(qlo, causal ? static_cast<int>(blockIdx.x) : 0) + wave; qt < qhi; qt += KS) {
     const int i0 = qt * 32;
     // This lane's 16 queries' softmax statistics, loaded first so their
     // latency overlaps the tile fills and QK^T.
@@ -1030,17 +1037,36 @@ __global__ __launch_bounds__(64 * KS) void attn_dv_f32_kernel(const float* __res
     }
   }
   if (key < S) {
+    float* part = split_qt > 0 ? ws + static_cast<size_t>(blockIdx.z) * gridDim.y * S * D + head : nullptr;
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int d = t * 32 + acc_row(r, lane);
         if (d < D) {
-          float* vp = v + static_cast<size_t>(key) * D + d;
-          *vp = *vp - lr * dv[t][r];
+          if (split_qt > 0) {
+            part[static_cast<size_t>(key) * D + d] = dv[t][r];
+          } else {
+            float* vp = v + static_cast<size_t>(key) * D + d;
+            *vp = *vp - lr * dv[t][r];
+          }
         }
       }
     }
+  }
+}
+
+// Sums attn_dv_f32_kernel's query splits in split order and applies
+// V -= lr * dV, one thread per element of V.
+__global__ __launch_bounds__(256) void attn_dv_split_combine_kernel(const float* __restrict__ ws, float* __restrict__ v,
+                                                                    size_t n, int nsplit, float lr) {
+  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<size_t>(gridDim.x) * 256) {
+    float acc = 0.0f;
+    for (int z = 0; z < nsplit; ++z) {
+      acc += ws[static_cast<size_t>(z) * n + i];
+    }
+    v[i] = v[i] - lr * acc;
   }
 }
 
@@ -1194,12 +1220,21 @@ __global__ __launch_bounds__(64 * KS) void attn_dv_f32_q16_kernel(const float* _
 
 // loss = sum over n elements of (out - target)^2 * norm, one workgroup,
 // fixed reduction order (deterministic).
+// Workgroup b sums the squared differences of its contiguous chunk
+// [b, b + 1) * chunk (each thread strided through it, eight loads in flight,
+// then a tree over the threads) and stores the partial; the last workgroup to
+// finish (device-scope counter, reset by it) adds the partials in workgroup
+// order.  The same n and grid always give the same bits.
 __global__ __launch_bounds__(1024) void mse_loss_kernel(const float* __restrict__ out,
-                                                        const float* __restrict__ target, size_t n, float norm,
-                                                        float* __restrict__ loss) {
+                                                        const float* __restrict__ target, size_t n, size_t chunk,
+                                                        float norm, float* __restrict__ loss,
+                                                        float* __restrict__ partials, unsigned* __restrict__ counter) {
   __shared__ float part[1024];
+  const size_t lo = static_cast<size_t>(blockIdx.x) * chunk;
+  const size_t hi = lo + chunk < n ? lo + chunk : n;
   float acc = 0.0f;
-  for (size_t i = threadIdx.x; i < n; i += 1024) {
+#pragma unroll 8
+  for (size_t i = lo + threadIdx.x; i < hi; i += 1024) {
     const float d = out[i] - target[i];
     acc += d * d;
   }
@@ -1211,8 +1246,22 @@ __global__ __launch_bounds__(1024) void mse_loss_kernel(const float* __restrict_
     }
     __syncthreads();
   }
+  if (gridDim.x == 1) {
+    if (threadIdx.x == 0) {
+      *loss = part[0] * norm;
+    }
+    return;
+  }
   if (threadIdx.x == 0) {
-    *loss = part[0] * norm;
+    __hip_atomic_store(&partials[blockIdx.x], part[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__hip_atomic_fetch_add(counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) == gridDim.x - 1) {
+      float total = 0.0f;
+      for (unsigned b = 0; b < gridDim.x; ++b) {
+        total += __hip_atomic_load(&partials[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      *loss = total * norm;
+      __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
@@ -2230,9 +2279,22 @@ hipError_t convAttentionF32(const float* x, const float* w, const float* bias, i
   return hipGetLastError();
 }
 
+size_t attentionDvWorkspaceFloats(int bh, int S, int D, int splits) {
+  if (D <= 0 || D > 256 || S <= 0 || bh <= 0 || q16Serves(bh, S, D, splits)) {
+    return 0;
+  }
+  const int ks = attentionF32Splits(bh, S, D, splits == kAttnF32Q16 ? 0 : splits);
+  const int tiles = keySplitTiles(bh, S, ks);
+  if (tiles == 0) {
+    return 0;
+  }
+  const int nqt = (S + 31) / 32;
+  return static_cast<size_t>((nqt + tiles - 1) / tiles) * bh * S * D;
+}
+
 hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const float* out, const float* target,
                                 const float* stats, int bh, int S, int D, bool causal, float lr,
-                                hipStream_t stream, int splits) {
+                                hipStream_t stream, int splits, float* split_ws, size_t split_ws_floats) {
   if (D <= 0 || D > 256 || S <= 0 || bh <= 0) {
     return hipErrorInvalidValue;
   }
@@ -2257,14 +2319,21 @@ hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const 
     return hipGetLastError();
   }
   const int nkb = (S + 31) / 32;
-  const dim3 grid(nkb, bh);
   const int dt = (D + 31) / 32;
   // Query-tile splits: the same rule and LDS limits as the forward's key
   // splits (K tile + per-wave Q / dO tiles).
   const int ks = attentionF32Splits(bh, S, D, splits == kAttnF32Q16 ? 0 : splits);
+  // Small grids also divide each key block's query tiles among workgroups
+  // (the forward's rule), when the caller's workspace holds the partials.
+  int split_qt = keySplitTiles(bh, S, ks);
+  const int nsplit = split_qt > 0 ? (nkb + split_qt - 1) / split_qt : 1;
+  if (split_qt > 0 && (split_ws == nullptr || split_ws_floats < static_cast<size_t>(nsplit) * bh * S * D)) {
+    split_qt = 0;
+  }
+  const dim3 grid(nkb, bh, split_qt > 0 ? nsplit : 1);
 #define LC_DV_F32(DT_, KS_)                                                                                         \
   hipLaunchKernelGGL((attn_dv_f32_kernel<DT_, KS_>), grid, dim3(64 * (KS_)), 0, stream, q, k, v, out, target, stats, \
-                     S, D, cz, scale, lr)
+                     S, D, cz, scale, lr, split_qt, split_ws)
 #define LC_DV_F32_KS(DT_)                                                                                           \
   switch (ks) {                                                                                                     \
     case 8: LC_DV_F32(DT_, (DT_ <= 2 ? 8 : 1)); break;                                                              \
@@ -2284,14 +2353,32 @@ hipError_t attentionDvUpdateF32(const float* q, const float* k, float* v, const 
   }
 #undef LC_DV_F32_KS
 #undef LC_DV_F32
+  if (split_qt > 0) {
+    const size_t n = static_cast<size_t>(bh) * S * D;
+    const size_t blocks = (n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096;
+    hipLaunchKernelGGL(attn_dv_split_combine_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream,
+                       split_ws, v, n, nsplit, lr);
+  }
   return hipGetLastError();
 }
 
-hipError_t mseLossF32(const float* out, const float* target, size_t n, float norm, float* loss, hipStream_t stream) {
+hipError_t mseLossF32(const float* out, const float* target, size_t n, float norm, float* loss, hipStream_t stream,
+                      float* partials, unsigned* counter) {
   if (n == 0) {
     return hipErrorInvalidValue;
   }
-  hipLaunchKernelGGL(mse_loss_kernel, dim3(1), dim3(1024), 0, stream, out, target, n, norm, loss);
+  // 16384 elements per workgroup, at most kMseLossMaxBlocks of them (one
+  // workgroup without the scratch).
+  size_t blocks = (n + 16383) / 16384;
+  if (blocks > static_cast<size_t>(kMseLossMaxBlocks)) {
+    blocks = kMseLossMaxBlocks;
+  }
+  if (partials == nullptr || counter == nullptr) {
+    blocks = 1;
+  }
+  const size_t chunk = (n + blocks - 1) / blocks;
+  hipLaunchKernelGGL(mse_loss_kernel, dim3(static_cast<unsigned>(blocks)), dim3(1024), 0, stream, out, target, n,
+                     chunk, norm, loss, partials, counter);
   return hipGetLastError();
 }
 
