@@ -296,8 +296,13 @@ Status attentionForwardQuick(HipContext* ctx, AttnResident& res, const AttnShape
   std::memcpy(stage, q, bytes);
   std::memcpy(stage + n, k, bytes);
   std::memcpy(stage + 2 * n, v, bytes);
-  const hipError_t ce = kern::split3CopyF32(static_cast<const float*>(ctx->pinned.device()), res.q.as<float>(),
-                                            res.k.as<float>(), res.v.as<float>(), n, ctx->stream);
+  const float* dev = static_cast<const float*>(ctx->pinned.device());
+  kern::CopySegsF32 in{};
+  in.seg[0] = kern::CopySegF32{dev, res.q.as<float>(), n};
+  in.seg[1] = kern::CopySegF32{dev + n, res.k.as<float>(), n};
+  in.seg[2] = kern::CopySegF32{dev + 2 * n, res.v.as<float>(), n};
+  in.count = 3;
+  const hipError_t ce = kern::copySegsF32(in, ctx->stream);
   if (ce != hipSuccess) {
     return failHip(ce, "attention input copy");
   }
@@ -408,6 +413,10 @@ Status attentionForwardResident(HipContext* ctx, AttnResident& res, const AttnSh
     }
   }
   res.has_out = true;
+  if (policy.download_out && n <= kStagedDownloadMax && quickAttnEnabled()) {
+    const StagedOut o{res.out.as<float>(), out, n};
+    return stagedDownload(ctx, &o, 1);
+  }
   if (policy.download_out) {
     LC_TRY(download(ctx, out, res.out.get(), n * sizeof(float)));
   }
@@ -444,25 +453,54 @@ Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShap
   }
   const std::size_t n = sh.elems();
   const std::size_t bytes = n * sizeof(float);
+  // Plain steps of small problems (every input uploaded, out and V downloaded):
+  // staged through pinned memory by copy kernels, the wait on the completion
+  // flag, as the plain forward (attentionForwardQuick).
+  const bool quick = policy.upload_q && policy.upload_k && policy.upload_v && policy.upload_target &&
+                     policy.download_out && policy.download_v && n <= kQuickAttnElems && quickAttnEnabled();
+  const std::size_t n4 = roundUp(n, 64);  // 256-byte aligned staging slots
+  float* stage = nullptr;
+  const float* stage_dev = nullptr;
+  if (quick) {
+    LC_TRY(ctx->pinned.ensure((6 * n4 + 64) * sizeof(float)));
+    stage = static_cast<float*>(ctx->pinned.get());
+    stage_dev = static_cast<const float*>(ctx->pinned.device());
+    std::memcpy(stage, q, bytes);
+    std::memcpy(stage + n4, k, bytes);
+    std::memcpy(stage + 2 * n4, v, bytes);
+    std::memcpy(stage + 3 * n4, target, bytes);
+  }
   if (policy.upload_q) {
     LC_TRY(res.q.ensure(bytes));
-    LC_TRY(upload(ctx, res.q.get(), q, bytes));
+    if (!quick) LC_TRY(upload(ctx, res.q.get(), q, bytes));
     res.has_q = true;
   }
   if (policy.upload_k) {
     LC_TRY(res.k.ensure(bytes));
-    LC_TRY(upload(ctx, res.k.get(), k, bytes));
+    if (!quick) LC_TRY(upload(ctx, res.k.get(), k, bytes));
     res.has_k = true;
   }
   if (policy.upload_v) {
     LC_TRY(res.v.ensure(bytes));
-    LC_TRY(upload(ctx, res.v.get(), v, bytes));
+    if (!quick) LC_TRY(upload(ctx, res.v.get(), v, bytes));
     res.has_v = true;
   }
   if (policy.upload_target) {
     LC_TRY(res.target.ensure(bytes));
-    LC_TRY(upload(ctx, res.target.get(), target, bytes));
+    if (!quick) LC_TRY(upload(ctx, res.target.get(), target, bytes));
     res.has_target = true;
+  }
+  if (quick) {
+    kern::CopySegsF32 in{};
+    in.seg[0] = kern::CopySegF32{stage_dev, res.q.as<float>(), n};
+    in.seg[1] = kern::CopySegF32{stage_dev + n4, res.k.as<float>(), n};
+    in.seg[2] = kern::CopySegF32{stage_dev + 2 * n4, res.v.as<float>(), n};
+    in.seg[3] = kern::CopySegF32{stage_dev + 3 * n4, res.target.as<float>(), n};
+    in.count = 4;
+    const hipError_t ce = kern::copySegsF32(in, ctx->stream);
+    if (ce != hipSuccess) {
+      return failHip(ce, "attention train step input copy");
+    }
   }
   LC_TRY(res.out.ensure(bytes));
   LC_TRY(res.stats.ensure(sh.seq_len * 2 * sizeof(float)));
@@ -495,6 +533,38 @@ Status attentionTrainResident(HipContext* ctx, AttnResident& res, const AttnShap
     return failHip(e, "attention train step launch");
   }
   res.has_out = true;
+  if (quick) {
+    unsigned* flag_dev = nullptr;
+    unsigned* count_dev = nullptr;
+    unsigned seq = 0;
+    LC_TRY(prepareDoneFlag(ctx, &flag_dev, &count_dev, &seq));
+    float* odev = static_cast<float*>(ctx->pinned.device());
+    kern::CopySegsF32 outs{};
+    outs.seg[0] = kern::CopySegF32{res.out.as<float>(), odev + 4 * n4, n};
+    outs.seg[1] = kern::CopySegF32{res.v.as<float>(), odev + 5 * n4, n};
+    outs.seg[2] = kern::CopySegF32{res.loss.as<float>(), odev + 6 * n4, 1};
+    outs.count = loss_out != nullptr ? 3 : 2;
+    const hipError_t ce = kern::copySegsF32(outs, ctx->stream, count_dev, flag_dev, seq);
+    if (ce != hipSuccess) {
+      return failHip(ce, "attention train step output copy");
+    }
+    LC_TRY(waitDoneFlag(ctx, seq));
+    std::memcpy(out, stage + 4 * n4, bytes);
+    std::memcpy(v, stage + 5 * n4, bytes);
+    if (loss_out != nullptr) {
+      *loss_out = stage[6 * n4];
+    }
+    return Status::kSuccess;
+  }
+  if ((policy.download_out || policy.download_v || loss_out != nullptr) && quickAttnEnabled() &&
+      (n <= kStagedDownloadMax || (!policy.download_out && !policy.download_v))) {
+    StagedOut o[3];
+    int count = 0;
+    if (policy.download_out) o[count++] = StagedOut{res.out.as<float>(), out, n};
+    if (policy.download_v) o[count++] = StagedOut{res.v.as<float>(), v, n};
+    if (loss_out != nullptr) o[count++] = StagedOut{res.loss.as<float>(), loss_out, 1};
+    return stagedDownload(ctx, o, count);
+  }
   if (policy.download_out) {
     LC_TRY(download(ctx, out, res.out.get(), bytes));
   }

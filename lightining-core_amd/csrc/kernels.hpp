@@ -68,9 +68,20 @@ hipError_t gemmF32ConvNchw(const float* cols, const float* Wt, float* out, int M
 // row = (n*oh + oy)*ow + ox, col = (c*kh + ky)*kw + kx.
 hipError_t im2colF32(const float* x, float* cols, int batch, int C, int H, int W, int kh, int kw, int sh, int sw,
                      int ph, int pw, int oh, int ow, hipStream_t stream);
-// d0 / d1 / d2 [0, n) = src [0, n) / [n, 2n) / [2n, 3n); src may be the device
-// alias of pinned host memory (read once).
-hipError_t split3CopyF32(const float* src, float* d0, float* d1, float* d2, size_t n, hipStream_t stream);
+// Up to four copies dst[0, n) = src[0, n) in one launch (either side may be the
+// device alias of pinned host memory); with done_flag / done_count, the
+// launch's completion flag as for attentionF32.
+struct CopySegF32 {
+  const float* src;
+  float* dst;
+  size_t n;
+};
+struct CopySegsF32 {
+  CopySegF32 seg[4];
+  int count;
+};
+hipError_t copySegsF32(const CopySegsF32& segs, hipStream_t stream, unsigned* done_count = nullptr,
+                       unsigned* done_flag = nullptr, unsigned done_seq = 0);
 // dst [0, n) = src [0, n), dst being the device alias of pinned host memory;
 // then the launch's last workgroup writes done_seq to *done_flag (host-mapped)
 // once every value is visible to the host, and leaves *done_count (device,

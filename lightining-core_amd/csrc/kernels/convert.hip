@@ -163,40 +163,25 @@ __global__ __launch_bounds__(256) void repeat_fill_kernel(const float* __restric
   }
 }
 
-// dst_j[i] = src[j * n + i], j = 0, 1, 2: three tensors packed back to back
-// (in mapped host memory: each value crosses the bus once) into three
-// buffers.  VEC: n % 4 == 0 and every base 16-byte aligned.
-template <bool VEC>
-__global__ __launch_bounds__(256) void split3_copy_f32_kernel(const float* __restrict__ src, float* __restrict__ d0,
-                                                              float* __restrict__ d1, float* __restrict__ d2,
-                                                              size_t n) {
-  const size_t w = VEC ? n / 4 : n;
-  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < 3 * w;
-       i += static_cast<size_t>(gridDim.x) * 256) {
-    const size_t j = i / w;
-    const size_t r = i - j * w;
-    float* d = j == 0 ? d0 : j == 1 ? d1 : d2;
-    if (VEC) {
-      reinterpret_cast<float4*>(d)[r] = reinterpret_cast<const float4*>(src)[i];
+// Copies up to four (src, dst, n) segments in one launch: a small call's
+// inputs out of mapped pinned staging (each value crosses the bus once), or
+// its results into it.  Segment c runs as float4 when its n % 4 == 0 and both
+// bases are 16-byte aligned.  With a completion flag, every wave releases its
+// stores before the workgroup is counted.
+__global__ __launch_bounds__(256) void copy_segs_f32_kernel(kern::CopySegsF32 segs, DoneFlag done) {
+  const size_t stride = static_cast<size_t>(gridDim.x) * 256;
+  const size_t first = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x;
+  for (int c = 0; c < segs.count; ++c) {
+    const kern::CopySegF32 sg = segs.seg[c];
+    const bool vec = sg.n % 4 == 0 && (reinterpret_cast<uintptr_t>(sg.src) | reinterpret_cast<uintptr_t>(sg.dst)) % 16 == 0;
+    if (vec) {
+      for (size_t i = first; i < sg.n / 4; i += stride) {
+        reinterpret_cast<float4*>(sg.dst)[i] = reinterpret_cast<const float4*>(sg.src)[i];
+      }
     } else {
-      d[r] = src[i];
-    }
-  }
-}
-
-// dst[i] = src[i] for i < n into the device alias of pinned host memory, then
-// the launch's completion flag.  VEC: n % 4 == 0 and both bases 16-byte
-// aligned.
-template <bool VEC>
-__global__ __launch_bounds__(256) void copy_out_flag_kernel(const float* __restrict__ src, float* __restrict__ dst,
-                                                            size_t n, DoneFlag done) {
-  const size_t w = VEC ? n / 4 : n;
-  for (size_t i = static_cast<size_t>(blockIdx.x) * 256 + threadIdx.x; i < w;
-       i += static_cast<size_t>(gridDim.x) * 256) {
-    if (VEC) {
-      reinterpret_cast<float4*>(dst)[i] = reinterpret_cast<const float4*>(src)[i];
-    } else {
-      dst[i] = src[i];
+      for (size_t i = first; i < sg.n; i += stride) {
+        sg.dst[i] = sg.src[i];
+      }
     }
   }
   done.finish_all_writers();
@@ -333,18 +318,28 @@ hipError_t repeatFillF32(const float* src, size_t n, float* dst, size_t total, h
   return hipGetLastError();
 }
 
-hipError_t split3CopyF32(const float* src, float* d0, float* d1, float* d2, size_t n, hipStream_t stream) {
-  if (n == 0) {
-    return hipSuccess;
+hipError_t copySegsF32(const CopySegsF32& segs, hipStream_t stream, unsigned* done_count, unsigned* done_flag,
+                       unsigned done_seq) {
+  if (segs.count < 1 || segs.count > 4 || (done_flag != nullptr && done_count == nullptr)) {
+    return hipErrorInvalidValue;
   }
-  const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(d0) |
-                                  reinterpret_cast<uintptr_t>(d1) | reinterpret_cast<uintptr_t>(d2)) % 16 == 0;
-  const size_t items = 3 * (vec ? n / 4 : n);
-  if (vec) {
-    hipLaunchKernelGGL(split3_copy_f32_kernel<true>, dim3(grid_for(items)), dim3(256), 0, stream, src, d0, d1, d2, n);
-  } else {
-    hipLaunchKernelGGL(split3_copy_f32_kernel<false>, dim3(grid_for(items)), dim3(256), 0, stream, src, d0, d1, d2, n);
+  // Threads for the longest segment (float4 items where it vectorises), at
+  // most 64 workgroups: with a flag, every workgroup is one more device-scope
+  // count on the last one's path.
+  size_t items = 0;
+  for (int c = 0; c < segs.count; ++c) {
+    const CopySegF32& sg = segs.seg[c];
+    const bool vec = sg.n % 4 == 0 &&
+                     (reinterpret_cast<uintptr_t>(sg.src) | reinterpret_cast<uintptr_t>(sg.dst)) % 16 == 0;
+    const size_t w = vec ? sg.n / 4 : sg.n;
+    items = w > items ? w : items;
   }
+  if (items == 0) {
+    return hipErrorInvalidValue;
+  }
+  const int grid = grid_for(items) < 64 ? grid_for(items) : 64;
+  hipLaunchKernelGGL(copy_segs_f32_kernel, dim3(grid), dim3(256), 0, stream, segs,
+                     DoneFlag{done_count, done_flag, done_seq});
   return hipGetLastError();
 }
 
@@ -353,16 +348,10 @@ hipError_t copyOutFlagF32(const float* src, float* dst, size_t n, unsigned* done
   if (n == 0 || done_count == nullptr || done_flag == nullptr) {
     return hipErrorInvalidValue;
   }
-  const DoneFlag done{done_count, done_flag, done_seq};
-  const bool vec = n % 4 == 0 && (reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst)) % 16 == 0;
-  const size_t items = vec ? n / 4 : n;
-  const int grid = grid_for(items) < 256 ? grid_for(items) : 256;
-  if (vec) {
-    hipLaunchKernelGGL(copy_out_flag_kernel<true>, dim3(grid), dim3(256), 0, stream, src, dst, n, done);
-  } else {
-    hipLaunchKernelGGL(copy_out_flag_kernel<false>, dim3(grid), dim3(256), 0, stream, src, dst, n, done);
-  }
-  return hipGetLastError();
+  CopySegsF32 segs{};
+  segs.seg[0] = CopySegF32{src, dst, n};
+  segs.count = 1;
+  return copySegsF32(segs, stream, done_count, done_flag, done_seq);
 }
 
 }  // namespace lchip::kern

@@ -412,6 +412,10 @@ Status matmulResident(HipContext* ctx, MatMulResident& r, std::size_t m, std::si
     }
   }
   r.has_c = true;
+  if (policy.download_out && m * n <= kStagedDownloadMax && quickMatMulEnabled()) {
+    const StagedOut o{r.c.as<float>(), out, m * n};
+    return stagedDownload(ctx, &o, 1);
+  }
   if (policy.download_out) {
     LC_TRY(download(ctx, out, r.c.get(), m * n * sizeof(float)));
   }

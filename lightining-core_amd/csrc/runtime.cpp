@@ -329,6 +329,39 @@ Status waitDoneFlag(HipContext* ctx, unsigned seq) {
   return Status::kSuccess;
 }
 
+// Synchronous downloads of small results: one kernel copies the device buffers into the pinned staging and
+// raises the completion flag; the host waits on the flag and copies out.  A
+// pageable download and a stream sync cost ~10 us each at these sizes.
+Status stagedDownload(HipContext* ctx, const StagedOut* outs, int count) {
+  std::size_t at[4] = {0, 0, 0, 0};
+  std::size_t total = 0;
+  for (int c = 0; c < count; ++c) {
+    at[c] = total;
+    total += roundUp(outs[c].n, 64);
+  }
+  LC_TRY(ctx->pinned.ensure(total * sizeof(float)));
+  unsigned* flag_dev = nullptr;
+  unsigned* count_dev = nullptr;
+  unsigned seq = 0;
+  LC_TRY(prepareDoneFlag(ctx, &flag_dev, &count_dev, &seq));
+  float* dev = static_cast<float*>(ctx->pinned.device());
+  kern::CopySegsF32 segs{};
+  for (int c = 0; c < count; ++c) {
+    segs.seg[c] = kern::CopySegF32{outs[c].src, dev + at[c], outs[c].n};
+  }
+  segs.count = count;
+  const hipError_t e = kern::copySegsF32(segs, ctx->stream, count_dev, flag_dev, seq);
+  if (e != hipSuccess) {
+    return failHip(e, "staged download copy");
+  }
+  LC_TRY(waitDoneFlag(ctx, seq));
+  const float* stage = static_cast<const float*>(ctx->pinned.get());
+  for (int c = 0; c < count; ++c) {
+    std::memcpy(outs[c].dst, stage + at[c], outs[c].n * sizeof(float));
+  }
+  return Status::kSuccess;
+}
+
 Status noteEnqueued(HipContext* ctx, TraceOp op, std::size_t launches) {
   const bool mm = op == TraceOp::kMatMul;
   std::size_t& count = mm ? ctx->matmul_inflight : ctx->attention_inflight;

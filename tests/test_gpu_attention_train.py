@@ -91,6 +91,31 @@ def test_train_steps_on_resident_v(lc, oracle):
     sess.close()
 
 
+def test_plain_steps_in_a_row_then_resident_steps(lc, oracle):
+    # Plain steps (every input uploaded, out and V downloaded) of up to 65536
+    # values per tensor stage through pinned memory and wait on a completion
+    # flag; a row of them with changing shapes, mixed with plain forward calls
+    # that share the staging and the flag, each matches the oracle, and the V
+    # a plain step leaves on the device feeds the next resident step.
+    shapes = [(256, 64, False, 2.0), (100, 33, True, 5.0), (7, 5, False, 1.0), (255, 256, True, 20.0),
+              (256, 64, True, 2.0)]
+    for i, (s, d, causal, lr) in enumerate(shapes):
+        q, k, v, t = (synth.normal((s, d), stream=900 + 4 * i + j) for j in range(4))
+        sess = lc.AttentionSession(s, d, causal=causal)
+        got = sess.train_step(q, k, v, t, lr)
+        _check_step(f"plain step {i}: S={s} D={d} causal={causal}", oracle.attention_train_step(q, k, v, t, lr, causal),
+                    got, v)
+        fq, fk, fv = (synth.normal((64, 32), stream=950 + 3 * i + j) for j in range(3))
+        assert_parity(oracle.attention(fq, fk, fv), lc.attention2d(fq, fk, fv), "f32", f"forward between steps {i}")
+        if i == len(shapes) - 1:
+            v1 = np.asarray(got[1], np.float32).reshape(s, d)
+            keep = lc.AttentionIoPolicy(upload_q=False, upload_k=False, upload_v=False, upload_target=False)
+            got2 = sess.train_step_with_policy(q, k, v, t, lr, keep)
+            _check_step("resident step after a plain one", oracle.attention_train_step(q, k, v1, t, lr, causal), got2,
+                        v1)
+        sess.close()
+
+
 @pytest.mark.parametrize("s,d,causal", [(256, 64, False), (100, 48, True)])
 def test_train_run_cached_matches_steps(lc, s, d, causal):
     # train_run_cached(lr, n) (the C loop of resident steps) leaves the same V
