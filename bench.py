@@ -285,6 +285,18 @@ def bench_config2(lc, synth, cpu):
     kflops = 2.0 * 1024 ** 3
     achieved = kflops / (kms * 1e-3) / 1e12
     entry = extra_entry("C2", flops_step, ms_per_step, "f32")
+    # 1024^3 as one plain API call on host arrays (the form of the
+    # reference's published one-shot figures): median wall time of lc.matmul2d.
+    a0, b0 = inputs[0]
+    for _ in range(5):
+        lc.matmul2d(a0, b0)
+    per_call = []
+    for _ in range(40):
+        t0 = time.perf_counter()
+        lc.matmul2d(a0, b0)
+        per_call.append(time.perf_counter() - t0)
+    per_call.sort()
+    entry["one_shot_ms_per_call_1024^3"] = round(per_call[len(per_call) // 2] * 1e3, 5)
     entry["kernel_1024^3"] = {"kernel": "gemm_f32_lds_kernel<64,2,2> (v_mfma_f32_32x32x2_f32)",
                               "avg_kernel_ms": round(kms, 5), "TFLOP/s": round(achieved, 3),
                               "frac_peak": round(achieved / PEAK_TFLOPS["f32"], 4),
@@ -347,6 +359,18 @@ def bench_extras(lc, synth, cpu):
         sample = f"{n} full forwards in {el:.2f} s, 1 thread ({cpu.kind})"
     out["C1_attention_f32_S256_D64"] = extra_entry("C1", 4.0 * s * s * d, ms, "f32", cpu_tf, sample)
     sess.close()
+    # The same problem as one plain API call on host arrays (the form of the
+    # reference's published per-call figure): median wall time of lc.attention2d.
+    for _ in range(20):
+        lc.attention2d(q, k, v, False)
+    per_call = []
+    for _ in range(200):
+        t0 = time.perf_counter()
+        lc.attention2d(q, k, v, False)
+        per_call.append(time.perf_counter() - t0)
+    per_call.sort()
+    out["C1_attention_f32_S256_D64"]["one_shot_ms_per_call"] = round(per_call[len(per_call) // 2] * 1e3, 5)
+    out["C1_attention_f32_S256_D64"]["one_shot_includes"] = "host arrays in and out (lc.attention2d), median of 200"
 
     # T1 attention train step fp32 S=256 D=64 (the
     # reference's training shape, loss sampled every 32 steps as its
