@@ -70,6 +70,31 @@ def test_attention_f32_key_split(lc, oracle, s, d, causal):
     np.testing.assert_array_equal(lc.attention2d(q, k, v, causal), got)
 
 
+def test_attention_f32_seeded_shape_sweep(lc, oracle):
+    # 40 seeded shapes across the kernel choices (16-query kernel, 32-query
+    # kernel with and without key splits, float4 and scalar tile fills,
+    # plain-call staging and pageable copies), causal or not, with and
+    # without the output postprocess, each against the oracle.
+    rng = np.random.default_rng(20260401)
+    done = 0
+    while done < 40:
+        s = int(rng.integers(1, 2200))
+        d = int(rng.choice([1, 3, 4, 8, 16, 31, 32, 48, 64, 65, 96, 128, 160, 200, 255, 256]))
+        if s * s * d > 3e8:
+            continue
+        causal = bool(rng.integers(0, 2))
+        q, k, v = (synth.normal((s, d), stream=1000 + 3 * done + j) for j in range(3))
+        ref = oracle.attention(q, k, v, causal)
+        if rng.integers(0, 3) == 0:
+            pol = lc.AttentionIoPolicy(output_scale=1.5, output_bias=-0.25, output_relu=True)
+            got = lc.attention_forward_with_policy(q, k, v, s, d, causal, policy=pol).reshape(s, d)
+            ref = np.maximum(ref * 1.5 - 0.25, 0)
+        else:
+            got = lc.attention2d(q, k, v, causal)
+        assert_parity(ref, got, "f32", f"sweep {done}: S={s} D={d} causal={causal}")
+        done += 1
+
+
 def test_attention_f32_batched_key_split(lc, oracle):
     b, h, s, d = 1, 3, 300, 128
     q, k, v = (synth.normal((b, h, s, d), stream=820 + i) for i in range(3))
