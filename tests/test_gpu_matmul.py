@@ -226,6 +226,27 @@ def test_plain_calls_in_a_row_and_resident_reuse(lc, oracle):
     assert_parity(exp, again, "f32", "resident reuse after a plain call")
 
 
+def test_matmul_f32_seeded_shape_sweep(lc, oracle):
+    # 40 seeded fp32 shapes on both sides of the staging caps, as plain calls
+    # and as a resident session's start / run / finish (small results come
+    # back through the staged download), each against the oracle.
+    rng = np.random.default_rng(20260402)
+    for i in range(40):
+        m, k, n = (int(x) for x in rng.integers(1, 700, size=3))
+        a = synth.uniform((m, k), stream=1100 + 2 * i)
+        b = synth.uniform((k, n), stream=1101 + 2 * i)
+        ref = oracle.matmul(a, b)
+        if i % 2 == 0:
+            got = lc.matmul2d(a, b)
+        else:
+            s = lc.MatMulResidentSession(m, k, n, "f32")
+            s.start_into(a, b)
+            s.run_into()
+            got = s.finish_into().reshape(m, n)
+            s.close()
+        assert_parity(ref, got, "f32", f"sweep {i}: {m}x{k}x{n}")
+
+
 def test_trace_records_hip_dispatch(lc):
     lc.runtime_trace_clear()
     lc.runtime_trace_enable(True)
