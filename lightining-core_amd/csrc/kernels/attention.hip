@@ -88,22 +88,17 @@ struct AttnSrcConvRepeat {
     // coalesced pass, then LDS reads instead of dependent global loads per
     // multiply-add).
     if (staged()) {
+      // x, w and bias land back to back behind the output; one loop issues
+      // all of their loads before any wait, so a source in mapped host
+      // memory costs one PCIe round trip per workgroup instead of three.
       float* xb = buf + n;
-      float* wb = xb + xs;
-      float* bb = wb + ws;
-      for (int i = threadIdx.x; i < xs; i += nthreads) {
-        xb[i] = x[i];
-      }
-      for (int i = threadIdx.x; i < ws; i += nthreads) {
-        wb[i] = w[i];
-      }
-      if (bias != nullptr) {
-        for (int i = threadIdx.x; i < cout; i += nthreads) {
-          bb[i] = bias[i];
-        }
+      const int nb = bias != nullptr ? cout : 0;
+      const int tot = xs + ws + nb;
+      for (int i = threadIdx.x; i < tot; i += nthreads) {
+        xb[i] = i < xs ? x[i] : (i < xs + ws ? w[i - xs] : bias[i - xs - ws]);
       }
       __syncthreads();
-      conv(buf, xb, wb, bias != nullptr ? bb : nullptr, nthreads);
+      conv(buf, xb, xb + xs, nb != 0 ? xb + xs + ws : nullptr, nthreads);
     } else {
       conv(buf, x, w, bias, nthreads);
     }
