@@ -1019,7 +1019,9 @@ __global__ __launch_bounds__(64 * KS) void attn_dv_f32_kernel(const float* __res
     }
 #pragma unroll
     for (int t = 0; t < DT; ++t) {
-#pragma unroll
+      // Four rows at a time: fully unrolled over 16 rows x KS waves, the
+      // loads of KS = 8 push the kernel past its 256 registers into scratch.
+#pragma unroll 4
       for (int r = 0; r < 16; ++r) {
         const int idx = (t * 32 + acc_row(r, lane)) * 32 + (lane & 31);
         float acc = 0.0f;

@@ -2344,7 +2344,14 @@ static hipError_t launch_gemm_half_tile(HalfTile tile, LoadA load_a, const uint1
     case HalfTile::kBig8:
       return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
     case HalfTile::kBig4:
-      return launch_gemm_half_cfg<T, 256, 256, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
+      // With four waves each holds a 128 x 128 block; the QKV epilogue's
+      // address work on top of those 256 accumulators spills (1 KB per lane),
+      // so a forced big4 runs that epilogue with eight waves.
+      if constexpr (std::is_same_v<Epi, EpiQKV<T>>) {
+        return launch_gemm_half_cfg<T, 256, 256, 2, 4>(load_a, Bt, M, N, K, ldb, epi, stream);
+      } else {
+        return launch_gemm_half_cfg<T, 256, 256, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
+      }
     case HalfTile::kMid:
       return launch_gemm_half_cfg<T, 128, 128, 2, 2>(load_a, Bt, M, N, K, ldb, epi, stream);
     case HalfTile::kSmall:

@@ -28,7 +28,9 @@ half (s_ashr_i32 hi, lo, 31) instead of from the pointer.  The scan traces
 each copy's base pair back to its last writers and flags that shape.
 
 The scan checks every LDS-DMA load in the compiled kernels, and planted
-instances of the faulting sequences show the scan catches them.
+instances of the faulting sequences show the scan catches them.  The same
+compile also checks that no kernel spills to scratch (a nonzero private
+segment in its descriptor).
 """
 import concurrent.futures
 import glob
@@ -247,3 +249,13 @@ def test_built_kernels_have_no_lds_dma_hazards(tmp_path):
         problems += [f"{os.path.basename(out)}: {p}" for p in scan(text)]
     assert loads > 0, "no LDS-DMA loads found: the scan pattern no longer matches the kernels"
     assert not problems, "\n".join(problems[:20])
+    spills = []
+    kernels = 0
+    for out in outs:
+        for name, desc in re.findall(r"\.amdhsa_kernel (\S+)\n(.*?)\.end_amdhsa_kernel", open(out).read(), re.S):
+            kernels += 1
+            m = re.search(r"\.amdhsa_private_segment_fixed_size (\d+)", desc)
+            if m is None or int(m.group(1)) > 0:
+                spills.append(f"{os.path.basename(out)}: {name} private segment {m.group(1) if m else '?'} bytes")
+    assert kernels > 0, "no kernel descriptors found"
+    assert not spills, "\n".join(spills[:20])
