@@ -372,7 +372,7 @@ def bench_extras(lc, synth, cpu):
     out["C1_attention_f32_S256_D64"]["one_shot_ms_per_call"] = round(per_call[len(per_call) // 2] * 1e3, 5)
     out["C1_attention_f32_S256_D64"]["one_shot_includes"] = "host arrays in and out (lc.attention2d), median of 200"
 
-    # T1 attention train step fp32 S=256 D=64 (the
+    # T1 attention train step fp32 S=256 D=64 (the dV-only SGD step; the
     # reference's training shape, loss sampled every 32 steps as its
     # shape-aware default): V stays resident, nothing is downloaded.
     # Algorithmic work 6*S^2*D (forward 4, P^T . dO 2); the kernels also
@@ -436,7 +436,7 @@ def bench_extras(lc, synth, cpu):
     sess.close()
     del q, k, v
 
-    # the reference's conv -> attention hotspot shapes
+    # The reference's conv -> attention hotspot shapes
     # (README.md Pipeline Bench, "Integrated API ms" column: 0.396-0.431 ms on
     # its Apple GPU): conv n=1 c=3->16 h=w=8 k=3 pad 1 + ReLU, QkvPackRepeat,
     # attention.  One integrated API call per step, host arrays in and out, so
@@ -619,8 +619,8 @@ def main():
                          "fp32 GEMM (c2), or a few launches of each 16-bit config (bf16)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        log("bench.py: this build measures one GPU only (the path is single-GPU; see DESIGN.md for how it would "
-            "shard); run with --gpus 1")
+        log("bench.py: this build measures one GPU only (the path is single-GPU; sharding is a design note, not "
+            "built); run with --gpus 1")
         sys.exit(2)
 
     import lightning_core as lc

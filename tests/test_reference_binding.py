@@ -1,6 +1,6 @@
-"""The reference-side binding of INTEGRATION.md, compiled (CPU only).
+"""The reference-side binding of the integration guide, compiled (CPU only).
 
-INTEGRATION.md section 1 gives the `detail::` wrappers a maintainer adds to
+The guide's first section (the dispatcher hook) gives the `detail::` wrappers a maintainer adds to
 the reference tree (`attentionForwardHipWithPolicy`,
 `attentionTrainStepHipWithPolicy`, `matMulHipWithPolicy`).  This test takes
 that code block verbatim from the document and compiles it with g++ against
@@ -41,7 +41,7 @@ def _wrapper_block():
     text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     sec = text[text.index("## 1. C++ dispatcher hook"):]
     m = re.search(r"```cpp\n(.*?)```", sec, re.S)
-    assert m, "no C++ block in INTEGRATION.md section 1"
+    assert m, "no C++ block in the integration guide's dispatcher-hook section"
     block = m.group(1)
     assert "attentionForwardHipWithPolicy" in block and "matMulHipWithPolicy" in block
     return block
