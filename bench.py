@@ -11,6 +11,8 @@ by the library), timed on its own: launches back to back with a hipEvent
 pair around each; `cpu_baseline` is the reference's own
 matMulCpu (oracle/_ref/libref.so, single thread) on a row subset of the same
 bf16-rounded operands, scaled by rows (output rows are independent).
+`pcie_inclusive` is the same GEMM with A and B coming from host arrays and C
+going back to one (never the headline value).
 
 Also reported (`per_config`): every other BASELINE config on its own resident
 launch-only loop, each with TFLOP/s (or GB/s for the HBM-bound skinny GEMM)
@@ -233,6 +235,29 @@ def bench_headline(lc, synth, steps, warmup, cpu):
                 "kernel_ms_min_max": [round(float(per_launch.min()), 5), round(float(per_launch.max()), 5)],
                 "algorithmic_flops_per_launch": int(flops_step),
                 "algorithmic_bytes_per_launch": m * k * 2 + k * n * 2 + m * n * 4}
+    # PCIe-inclusive figure (never the headline value): the same GEMM with A
+    # and B coming from host arrays and C going back to one.  start_into
+    # uploads A and B (fp32, converted to bf16 on the device) and launches;
+    # finish_into launches again and downloads C.  One GEMM is charged for both
+    # crossings: flops / (t_start + t_finish - one kernel time); medians of 3.
+    out_h = np.empty(m * n, np.float32)
+    t_up, t_down = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        sess.start_into(a, b, out_h)
+        lc.device_synchronize()
+        t1 = time.perf_counter()
+        sess.finish_into(out=out_h)
+        t2 = time.perf_counter()
+        t_up.append(t1 - t0)
+        t_down.append(t2 - t1)
+    tu, td = sorted(t_up)[1], sorted(t_down)[1]
+    pcie = {"TFLOP/s": round(flops_step / (tu + td - kms * 1e-3) / 1e12, 3),
+            "upload_and_launch_ms": round(tu * 1e3, 3), "launch_and_download_ms": round(td * 1e3, 3),
+            "includes": "A and B (fp32 host arrays, 256 MiB each) to the device, C (256 MiB fp32) back; "
+                        "one GEMM charged"}
+    log(f"[bench] pcie-inclusive 8192^3: {pcie}")
+    del out_h
     cpu_obj = None
     if cpu.kind is not None:
         log(f"[bench] cpu baseline ({cpu.kind}) on config 5 8192^3 rows ...")
@@ -253,7 +278,7 @@ def bench_headline(lc, synth, steps, warmup, cpu):
                              f"in {el:.1f} s, single thread, -O3 -ffast-math -funroll-loops; rows are independent, "
                              f"so the full GEMM would take x{m / rows:.0f}: {el * m / rows:.0f} s"}
     sess.close()
-    return value, ms_per_step, roofline, cpu_obj
+    return value, ms_per_step, roofline, cpu_obj, pcie
 
 
 def bench_config2(lc, synth, cpu):
@@ -635,7 +660,7 @@ def main():
         pmc_workload(lc, synth, args.pmc_workload)
         return
     cpu = CpuBaseline()
-    value, ms_per_step, roofline, cpu_obj = bench_headline(lc, synth, args.steps, args.warmup, cpu)
+    value, ms_per_step, roofline, cpu_obj, pcie = bench_headline(lc, synth, args.steps, args.warmup, cpu)
     log(f"[bench] config5 8192^3: {value:.3f} TFLOP/s, {ms_per_step:.4f} ms/step, kernel {roofline}")
     extras = {} if args.no_extras else bench_extras(lc, synth, cpu)
     line = {
@@ -659,6 +684,7 @@ def main():
                    "hbm_bytes": info["total_memory_bytes"], "host": host_record()},
         "roofline": roofline,
         "cpu_baseline": cpu_obj,
+        "pcie_inclusive": pcie,
         "per_config": extras,
     }
     print(json.dumps(line), flush=True)
