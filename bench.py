@@ -565,10 +565,10 @@ PMC_GEMMS = 20
 # WRITE_SIZE: GEMM 4096.0 KiB/dispatch, copy 262144.0 KiB (x1.000).
 GEMM_F32_1024_TRAFFIC = 25235186 + 4194304  # HBM bytes per launch (fetch + write, calibrated)
 # 8192^3 bf16, HBM bytes per launch (fetch + write, calibrated), per kernel:
-# profiles/gemm_half_tn_w4h_kernel_8192cube_traffic.txt: FETCH_SIZE 787213.1 KiB/dispatch (x1.9998),
+# profiles/gemm_half_tn_w4h_kernel_8192cube_traffic.txt: FETCH_SIZE 787628.8 KiB/dispatch (x1.9998),
 # WRITE_SIZE 262144.0 KiB (x1.000).  A kernel without its own counter passes (a variant forced by
 # CJ_HIP_GEMM_TILE) reports null.
-GEMM_BF16_8192_TRAFFIC = {"gemm_half_tn_w4h_kernel": 1612060979 + 268435456}
+GEMM_BF16_8192_TRAFFIC = {"gemm_half_tn_w4h_kernel": 1612910685 + 268435456}
 
 
 def pmc_workload(lc, synth, which="c2"):
